@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""W4A16 GEMM benchmark on one MI355X (the BASELINE metric).
+
+Step = one M=1 decode token through the 7 GPTQ projections (q, k, v, o,
+gate, up, down) of 8 Llama-2-7B layers -- one pipeline stage of the
+reference's split model (BASELINE config 5's layer count) with the
+config-2 quantisation (group 128, asymmetric zeros).  The 56 packed weight
+matrices (842 MB) are distinct, four times the 256 MB Infinity Cache, so
+every launch streams its weights from HBM.  The step is captured once into
+a HIP graph and replayed; timing uses HIP events on the replay stream.
+
+Printed JSON line: ``value`` = algorithmic bytes moved per second (GB/s) at
+M=1, ``roofline`` for the decode kernel (the only kernel in the step),
+``prefill`` = the same 56 GEMMs at M=256 in TFLOP/s against the fp16 MFMA
+peak, ``cpu_baseline`` = the reference's CPU dequantise-then-matmul path
+(restated with torch CPU ops) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "drofell-for-revision_amd")
+sys.path[:0] = [REPO, PKG]
+
+METRIC = "W4A16 GEMM: HBM GB/s @M=1, TFLOP/s @M=256 (% MI355X roofline), 7B shapes"
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+GROUP = 128
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234):
+    import torch
+    from gptq_synth import LLAMA2_7B_SHAPES
+    from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
+
+    cache = CacheV2(dev)
+    tp = TuningParams(MAX_M=max_m)
+    gen = torch.Generator(device=dev)
+    mats = []
+    for layer in range(layers):
+        for pi, (name, (k, n)) in enumerate(LLAMA2_7B_SHAPES.items()):
+            gen.manual_seed(seed0 + 100 * layer + pi)
+            groups = k // GROUP
+            # uniform random words == every nibble uniform in 0..15
+            qweight = torch.randint(-2 ** 31, 2 ** 31, (k // 8, n), dtype=torch.int32,
+                                    device=dev, generator=gen)
+            qzeros = torch.randint(-2 ** 31, 2 ** 31, (groups, n // 8), dtype=torch.int32,
+                                   device=dev, generator=gen)
+            scales = (torch.randn(groups, n, device=dev, generator=gen).abs() * 0.01
+                      + 1e-3).to(torch.float16)
+            q4 = Q4MatrixV2(qweight, qzeros, scales, k, n, None, False, tp, cache)
+            mats.append((name, k, n, q4))
+            del qweight, qzeros, scales
+    cache.init_cache()
+    torch.cuda.synchronize()
+    return mats, cache
+
+
+def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None):
+    """Capture one pass over `mats` at M=m into a graph; return ms per pass."""
+    import torch
+
+    sel = [t for t in mats if select is None or select(t)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(m)
+    xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.float16)
+          for k in sorted({t[1] for t in sel})}
+    ys = {n: torch.empty(m, n, dtype=torch.float16, device=dev) for n in sorted({t[2] for t in sel})}
+
+    def one_pass():
+        for _, k, n, q4 in sel:
+            q4.matmul(xs[k], output=ys[n])
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        one_pass()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one_pass()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / steps
+    return ms, wall, sel
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference's CPU dequantise-then-matmul on one 4096x4096 projection."""
+    import statistics
+
+    import torch
+    from gptq_synth import algorithmic_bytes, make_layer, make_x
+    from oracle import cpu_path
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    lay = make_layer(4096, 4096, GROUP, seed=1000)
+    x = make_x(1, 4096, seed=1)
+    cpu_path.forward(x, lay.qweight, lay.qzeros, lay.scales, lay.g_idx)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter_ns()
+        cpu_path.forward(x, lay.qweight, lay.qzeros, lay.scales, lay.g_idx)
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    med = statistics.median(times)
+    nbytes = algorithmic_bytes(1, 4096, 4096, GROUP, False)
+    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"torch-CPU dequantise+matmul (real_quant.py:69-102 restated) of one "
+                       f"4096x4096 g128 asymmetric projection at M=1, {len(times)} runs, "
+                       f"median {med * 1e3:.1f} ms; torch {torch.__version__}")}
+
+
+def sweep(mats, dev, steps: int, warmup: int) -> None:
+    from gptq_synth import algorithmic_bytes, flops
+    for (k, n) in ((4096, 4096), (4096, 11008), (11008, 4096)):
+        for m in (1, 2, 4, 8, 16, 64, 256, 1024):
+            ms, _, sel = time_graph(mats, m, steps, warmup, dev,
+                                    select=lambda t, k=k, n=n: t[1] == k and t[2] == n)
+            per = ms / len(sel) * 1e3
+            b = algorithmic_bytes(m, k, n, GROUP, False)
+            f = flops(m, k, n)
+            log(json.dumps({"shape": f"{k}x{n}", "m": m, "us": round(per, 3),
+                            "GB/s": round(b / per / 1e3, 1), "TFLOP/s": round(f / per / 1e6, 2),
+                            "hbm_frac": round(b / per / 1e3 / HBM_PEAK_GBS, 4),
+                            "mfma_frac": round(f / per / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)}))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--prefill-m", type=int, default=256)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the W4A16 GEMM path has no multi-GPU leg in this build", file=sys.stderr)
+        return 2
+
+    import torch
+    from gptq_synth import LLAMA2_7B_SHAPES, algorithmic_bytes, flops
+
+    dev = torch.device("cuda", 0)
+    log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
+    mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1024 if args.sweep else 1))
+    weight_bytes = sum(q4.qweight.numel() * 4 + q4.scales.numel() * 2 + q4.qzeros.numel() * 4
+                       for _, _, _, q4 in mats)
+
+    torch.cuda.synchronize(dev)
+    ms, wall, _ = time_graph(mats, 1, args.steps, args.warmup, dev)
+    step_bytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"decode M=1: {ms * 1e3:.1f} us per step ({len(mats)} GEMMs), {gbs:.1f} GB/s, "
+        f"wall {wall:.3f} s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded random GPTQ int4 weights, N(0,1) fp16 activations)",
+        "config": {
+            "workload": ("llama2-7b 8-layer stage decode, 7 GPTQ projections per layer "
+                         "(4x 4096x4096, 2x 4096x11008, 1x 11008x4096), M=1, group 128, "
+                         "asymmetric zeros; 56 distinct weight matrices per step"),
+            "m": 1, "layers": args.layers, "group_size": GROUP,
+            "weight_bytes": weight_bytes, "algorithmic_bytes_per_step": step_bytes,
+            "launches_per_step": len(mats), "hip_graph": True,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+
+    traffic_file = os.path.join(REPO, "profiles", "decode_traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as f:
+            result["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+
+    if not args.no_prefill:
+        m = args.prefill_m
+        pms, _, _ = time_graph(mats, m, max(5, args.steps // 5), max(2, args.warmup // 5), dev)
+        pflop = sum(flops(m, k, n) for _, k, n, _ in mats)
+        tf = pflop / (pms * 1e-3) / 1e12
+        log(f"prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
+        result["prefill"] = {"m": m, "value": round(tf, 2), "unit": "TFLOP/s",
+                             "ms_per_step": round(pms, 5),
+                             "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
+                             "peak": MFMA_FP16_PEAK_TFLOPS, "bound": "mfma"}
+
+    if args.sweep:
+        sweep(mats, dev, max(5, args.steps // 5), 3)
+
+    if not args.no_cpu:
+        log("timing CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,254 @@
+// C ABI of libdrofell_w4a16.so (declared in include/drofell_w4a16.h).
+//
+// Validation and dispatch live here; the kernels are in w4a16_kernels.hip.
+// Every entry point returns a status code; nothing throws across the ABI.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <vector>
+
+#include "drofell_w4a16.h"
+#include "w4a16_internal.h"
+
+namespace {
+
+using dw4::kChunkK;
+using dw4::kStripN;
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // per-device property cache (0 = unknown)
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int v = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    g_cu_count[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_shape(int k, int n, int group_size) {
+  if (k <= 0 || n <= 0 || group_size <= 0) return DW4_ERR_INVALID_ARG;
+  if (k % kChunkK != 0 || n % kStripN != 0) return DW4_ERR_UNSUPPORTED;
+  if (group_size % 32 != 0 || k % group_size != 0) return DW4_ERR_UNSUPPORTED;
+  return DW4_OK;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? DW4_OK : DW4_ERR_LAUNCH; }
+
+// Prefill tiling and split-K factor for one call.  `ws_bytes` caps the
+// split count: with too little workspace the call runs unsplit.
+dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_bytes, bool cap_by_ws) {
+  dw4::PrefillPlan p;
+  p.bm = m <= 64 ? 64 : 128;
+  p.bn = 128;
+  const int kc = k / kChunkK;
+  const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
+  int splits = split_req;
+  if (splits <= 0) {
+    const int cus = cu_count();
+    splits = tiles >= cus ? 1 : cus / tiles;
+    splits = std::min(splits, std::max(1, kc / 4));
+    splits = std::min(splits, 16);
+  }
+  splits = std::max(1, std::min(splits, kc));
+  // the launcher rounds to whole chunks per split
+  const int cps = (kc + splits - 1) / splits;
+  splits = (kc + cps - 1) / cps;
+  if (cap_by_ws && splits > 1) {
+    const size_t per_split = (size_t)m * n * sizeof(float);
+    if ((size_t)splits * per_split > ws_bytes) splits = 1;
+  }
+  p.splits = splits;
+  return p;
+}
+
+bool use_decode(int path, int m) {
+  if (path == DW4_PATH_DECODE) return true;
+  if (path == DW4_PATH_PREFILL) return false;
+  return m <= dw4::kDecodeMaxM;
+}
+
+size_t workspace_for(int path, int m, int k, int n, int act_order) {
+  if (m <= 0) return 0;
+  if (use_decode(path, m)) return act_order ? (size_t)m * k * sizeof(uint16_t) : 0;
+  const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
+  return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dw4_abi_version(void) { return DW4_ABI_VERSION; }
+
+const char* dw4_strerror(int status) {
+  switch (status) {
+    case DW4_OK: return "ok";
+    case DW4_ERR_INVALID_ARG: return "invalid argument (null pointer, non-positive size or bad stride)";
+    case DW4_ERR_UNSUPPORTED: return "unsupported shape: need K % 128 == 0, N % 16 == 0, group_size % 32 == 0 and K % group_size == 0";
+    case DW4_ERR_MISALIGNED: return "misaligned buffer: pointers must be 16-byte aligned and ldx a multiple of 8";
+    case DW4_ERR_BAD_GIDX: return "g_idx out of range or groups not of uniform size group_size";
+    case DW4_ERR_WORKSPACE: return "workspace too small for this call (see dw4_workspace_size)";
+    case DW4_ERR_LAUNCH: return "kernel launch failed";
+    case DW4_ERR_DEVICE: return "HIP device error";
+    default: return "unknown status";
+  }
+}
+
+int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
+                    size_t* packed_qweight_bytes, size_t* packed_scales_bytes,
+                    size_t* packed_zeros_bytes, size_t* perm_bytes, size_t* workspace_bytes) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (max_m < 0) return DW4_ERR_INVALID_ARG;
+  const size_t groups = (size_t)(k / group_size);
+  if (packed_qweight_bytes) *packed_qweight_bytes = (size_t)k * n / 2;
+  if (packed_scales_bytes) *packed_scales_bytes = groups * n * sizeof(uint16_t);
+  if (packed_zeros_bytes) *packed_zeros_bytes = groups * n / 2;
+  if (perm_bytes) *perm_bytes = act_order ? (size_t)k * sizeof(int32_t) : 0;
+  if (workspace_bytes) {
+    size_t ws = 0;
+    for (int m = 1; m <= max_m; ++m)
+      ws = std::max(ws, workspace_for(DW4_PATH_AUTO, m, k, n, act_order));
+    *workspace_bytes = ws;
+  }
+  return DW4_OK;
+}
+
+int dw4_workspace_size(int m, int k, int n, int group_size, int act_order, size_t* workspace_bytes) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (m < 0 || workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
+  *workspace_bytes = workspace_for(DW4_PATH_AUTO, m, k, n, act_order);
+  return DW4_OK;
+}
+
+int dw4_make_perm(int k, int group_size, const int32_t* g_idx_host, int32_t* perm_host) {
+  if (k <= 0 || group_size <= 0 || g_idx_host == nullptr || perm_host == nullptr)
+    return DW4_ERR_INVALID_ARG;
+  if (k % group_size != 0) return DW4_ERR_UNSUPPORTED;
+  const int groups = k / group_size;
+  std::vector<int> count(groups, 0);
+  for (int r = 0; r < k; ++r) {
+    const int g = g_idx_host[r];
+    if (g < 0 || g >= groups) return DW4_ERR_BAD_GIDX;
+    ++count[g];
+  }
+  for (int g = 0; g < groups; ++g)
+    if (count[g] != group_size) return DW4_ERR_BAD_GIDX;
+  // exclusive prefix, then rows placed in ascending original order per group
+  std::vector<int> next(groups, 0);
+  for (int g = 0, acc = 0; g < groups; ++g) {
+    next[g] = acc;
+    acc += count[g];
+  }
+  for (int r = 0; r < k; ++r) perm_host[next[g_idx_host[r]]++] = r;
+  return DW4_OK;
+}
+
+int dw4_repack(int k, int n, int group_size, const int32_t* qweight, const int32_t* qzeros,
+               const uint16_t* scales, const int32_t* perm, int32_t* packed_qweight,
+               int32_t* packed_zeros, uint16_t* packed_scales, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (!qweight || !qzeros || !scales || !packed_qweight || !packed_zeros || !packed_scales)
+    return DW4_ERR_INVALID_ARG;
+  if (!aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  const hipError_t e = dw4::launch_repack(
+      reinterpret_cast<const uint32_t*>(qweight), reinterpret_cast<const uint32_t*>(qzeros), scales,
+      perm, reinterpret_cast<uint32_t*>(packed_qweight), reinterpret_cast<uint32_t*>(packed_zeros),
+      packed_scales, k, n, k / group_size, static_cast<hipStream_t>(stream));
+  return status_of(e);
+}
+
+int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, const uint16_t* x,
+                  int64_t ldx, const int32_t* packed_qweight, const int32_t* packed_zeros,
+                  const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (path < DW4_PATH_AUTO || path > DW4_PATH_PREFILL || m < 0 || split_k < 0)
+    return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  if (!x || !packed_qweight || !packed_zeros || !packed_scales || !y) return DW4_ERR_INVALID_ARG;
+  if (ldx < k || ldy < n) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(x) || (ldx % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  const bool decode = use_decode(path, m);
+  if (decode && m > dw4::kDecodeMaxM) return DW4_ERR_INVALID_ARG;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dw4::GemmArgs a;
+  a.M = m;
+  a.K = k;
+  a.N = n;
+  a.gs = group_size;
+  a.G = k / group_size;
+  a.x = x;
+  a.ldx = ldx;
+  a.pq = reinterpret_cast<const uint32_t*>(packed_qweight);
+  a.pz = reinterpret_cast<const uint32_t*>(packed_zeros);
+  a.ps = packed_scales;
+  a.perm = perm;
+  a.bias = bias;
+  a.y = y;
+  a.ldy = ldy;
+
+  if (decode) {
+    if (perm != nullptr) {
+      const size_t need = (size_t)m * k * sizeof(uint16_t);
+      if (workspace == nullptr || workspace_bytes < need) return DW4_ERR_WORKSPACE;
+      if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
+      uint16_t* xg = static_cast<uint16_t*>(workspace);
+      hipError_t e = dw4::launch_gather_x(x, ldx, perm, xg, m, k, s);
+      if (e != hipSuccess) return DW4_ERR_LAUNCH;
+      a.x = xg;
+      a.ldx = k;
+      a.perm = nullptr;
+    }
+    return status_of(dw4::launch_decode(a, s));
+  }
+
+  dw4::PrefillPlan plan = plan_prefill(m, k, n, split_k, workspace ? workspace_bytes : 0, true);
+  float* part = nullptr;
+  if (plan.splits > 1) {
+    if (workspace == nullptr || !aligned16(workspace)) {
+      plan.splits = 1;
+    } else {
+      part = static_cast<float*>(workspace);
+    }
+  }
+  return status_of(dw4::launch_prefill(a, plan, part, s));
+}
+
+int dw4_gemm(int m, int k, int n, int group_size, const uint16_t* x, int64_t ldx,
+             const int32_t* packed_qweight, const int32_t* packed_zeros,
+             const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias, uint16_t* y,
+             int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  return dw4_gemm_path(DW4_PATH_AUTO, 0, m, k, n, group_size, x, ldx, packed_qweight, packed_zeros,
+                       packed_scales, perm, bias, y, ldy, workspace, workspace_bytes, stream);
+}
+
+int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
+                const int32_t* packed_zeros, const uint16_t* packed_scales, const int32_t* perm,
+                uint16_t* w, int64_t ldw, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (!packed_qweight || !packed_zeros || !packed_scales || !w) return DW4_ERR_INVALID_ARG;
+  if (ldw < n) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  const hipError_t e = dw4::launch_dequant(
+      reinterpret_cast<const uint32_t*>(packed_qweight),
+      reinterpret_cast<const uint32_t*>(packed_zeros), packed_scales, perm, w, ldw, k, n,
+      group_size, k / group_size, static_cast<hipStream_t>(stream));
+  return status_of(e);
+}
+
+}  // extern "C"

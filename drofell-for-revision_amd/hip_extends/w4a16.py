@@ -1,0 +1,288 @@
+"""HIP (gfx950) GPTQ W4A16 matrix objects behind the quantized-Linear API.
+
+Mirrors the role of the reference's ``cuda_extends/exllama.py`` (paths
+relative to ``/root/reference/After-Revision-DROFELL``):
+
+* :class:`TuningParams` -- ``exllama.py:22-46`` (dispatch knobs; the values
+  here are this library's own);
+* :class:`CacheV2` -- ``exllama.py:358-378`` (one shared, stream-ordered
+  buffer per device/decoder group, sized before ``init_cache``);
+* :class:`Q4MatrixV2` -- ``exllama.py:381-544`` (load-time repack in
+  ``__init__``, ``matmul`` with M-based dispatch, dequantised-weight
+  export, transposed product for the PEFT backward);
+* :class:`Q4LinearFunction` / :class:`Q4ForwardOnlyLinearFunction` --
+  ``exllama.py:649-696,730-740``.
+
+All device work goes through ``libdrofell_w4a16.so``; there is no CPU or
+PyTorch fallback for the forward product.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Any, Optional, Tuple
+
+import torch
+from torch.autograd import Function
+
+from . import _lib
+
+
+@dataclass
+class TuningParams:
+    # Flattened M at or below which the register-dequant decode kernel runs
+    # (at most 64: four 16-row MFMA tiles); above it the prefill kernel runs.
+    DECODE_MAX_M: int = 64
+    # Largest flattened M the shared workspace is sized for.  Larger calls
+    # still run, without split-K (and raise for act-order decode, which
+    # cannot run without its gather buffer).
+    MAX_M: int = 4096
+    # Prefill split-K factor; 0 lets the library choose from the tile count.
+    PREFILL_SPLIT_K: int = 0
+
+
+class CacheV2(object):
+    """Per-device shared workspace for every matrix of one decoder group.
+
+    ``update_workspace_size`` grows the requested size while matrices are
+    built; ``init_cache`` allocates it once.  ``temp_weight`` (an fp16 K*N
+    buffer for the dequantised weight used by the transposed product) is
+    allocated on first use only.
+    """
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = torch.device(device)
+        self.workspace_size: int = 0
+        self.temp_weight_size: int = 0
+        self._workspace: Optional[torch.Tensor] = None
+        self._temp_weight: Optional[torch.Tensor] = None
+        self.cache_created = False
+
+    def update_workspace_size(self, nbytes: int) -> None:
+        if nbytes > self.workspace_size:
+            self.cache_created = False
+            self.workspace_size = nbytes
+
+    def update_temp_weight_size(self, elements: int) -> None:
+        if elements > self.temp_weight_size:
+            self.temp_weight_size = elements
+            self._temp_weight = None
+
+    def init_cache(self) -> None:
+        # at least 16 bytes so the pointer is never null and always aligned
+        self._workspace = torch.empty(max(self.workspace_size, 16), dtype=torch.uint8,
+                                      device=self.device)
+        self.cache_created = True
+
+    @property
+    def workspace(self) -> torch.Tensor:
+        if not self.cache_created or self._workspace is None:
+            raise RuntimeError("CacheV2.init_cache() must run before the first matmul")
+        return self._workspace
+
+    @property
+    def temp_weight(self) -> torch.Tensor:
+        if self._temp_weight is None:
+            self._temp_weight = torch.empty((1, self.temp_weight_size), dtype=torch.float16,
+                                            device=self.device)
+        return self._temp_weight
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _aligned_rows(x2: torch.Tensor) -> torch.Tensor:
+    """A [M, K] fp16 view whose base is 16-byte aligned with ldx % 8 == 0."""
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+        if x2.data_ptr() % 16 != 0:
+            x2 = x2.clone()
+    return x2
+
+
+class Q4MatrixV2(object):
+    """One repacked GPTQ projection on a HIP device.
+
+    ``__init__`` performs the load-time repack (``dw4_make_perm`` on the host
+    for act-order, then ``dw4_repack`` on the current stream).  The packed
+    tensors have the same shapes, dtypes and byte counts as the GPTQ
+    buffers they replace, so a module can re-register them in place.
+    """
+
+    def __init__(self,
+                 qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                 height: int, width: int,
+                 g_idx: Optional[torch.Tensor], use_act: bool,
+                 tuning_params: TuningParams,
+                 cache: CacheV2) -> None:
+        if qweight.device.type != "cuda":
+            raise ValueError("Q4MatrixV2 weights must live on a HIP device")
+        if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+            raise TypeError("qweight and qzeros must be int32")
+        if scales.dtype != torch.float16:
+            raise TypeError("scales must be float16")
+        if tuple(qweight.shape) != (height // 8, width):
+            raise ValueError(f"qweight shape {tuple(qweight.shape)} != {(height // 8, width)}")
+        groups = scales.shape[0]
+        if height % groups != 0 or tuple(scales.shape) != (groups, width) \
+                or tuple(qzeros.shape) != (groups, width // 8):
+            raise ValueError("qzeros/scales shapes do not match qweight")
+        self.height = height
+        self.width = width
+        self.group_size = height // groups
+        self.device = qweight.device
+        self.tuning_params = tuning_params
+        self.cache = cache
+
+        perm: Optional[torch.Tensor] = None
+        if use_act:
+            if g_idx is None:
+                raise ValueError("act-order needs g_idx")
+            g_host = g_idx.detach().to("cpu", torch.int32).contiguous()
+            if g_host.numel() != height:
+                raise ValueError("g_idx must hold one entry per input row")
+            perm_host = torch.empty(height, dtype=torch.int32)
+            _lib.call("dw4_make_perm", height, self.group_size, g_host.data_ptr(),
+                      perm_host.data_ptr())
+            # g_idx == k // group_size sorts to the identity: no gather needed
+            if not torch.equal(perm_host, torch.arange(height, dtype=torch.int32)):
+                perm = perm_host.to(self.device)
+        self.use_act = perm is not None
+        self.perm: torch.Tensor = perm if perm is not None else \
+            torch.empty(0, dtype=torch.int32, device=self.device)
+
+        self.qweight = torch.empty_like(qweight, memory_format=torch.contiguous_format)
+        self.qzeros = torch.empty_like(qzeros, memory_format=torch.contiguous_format)
+        self.scales = torch.empty_like(scales, memory_format=torch.contiguous_format)
+        with torch.cuda.device(self.device):
+            _lib.call("dw4_repack", height, width, self.group_size,
+                      qweight.contiguous().data_ptr(), qzeros.contiguous().data_ptr(),
+                      scales.contiguous().data_ptr(), _ptr(perm),
+                      self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
+                      _stream(self.device))
+        sizes = _lib.query_sizes(height, width, self.group_size, self.use_act,
+                                 max(1, tuning_params.MAX_M))
+        cache.update_workspace_size(sizes["workspace"])
+        cache.update_temp_weight_size(height * width)
+        self.reconstructed_weight_float16: Optional[torch.Tensor] = None
+
+    # -- configuration -------------------------------------------------------
+    def set_tuning_params(self, tuning_params: TuningParams) -> None:
+        self.tuning_params = tuning_params
+
+    def get_weight_matrix_shape(self) -> Tuple[int, int]:
+        return (self.height, self.width)
+
+    # -- products ------------------------------------------------------------
+    def _path(self, m: int) -> int:
+        if m <= min(self.tuning_params.DECODE_MAX_M, 64):
+            return _lib.DW4_PATH_DECODE
+        return _lib.DW4_PATH_PREFILL
+
+    def matmul(self, x: torch.Tensor, output: Optional[torch.Tensor] = None,
+               bias: Optional[torch.Tensor] = None, path: Optional[int] = None) -> torch.Tensor:
+        """``x @ W (+ bias)`` for x [..., K]; fp16 compute, x's dtype out."""
+        if x.device != self.device:
+            raise ValueError(f"input on {x.device}, weights on {self.device}")
+        in_dtype = x.dtype
+        if in_dtype != torch.float16:
+            x = x.to(torch.float16)
+        outshape = x.shape[:-1] + (self.width,)
+        x2 = _aligned_rows(x.reshape(-1, self.height))
+        m = x2.shape[0]
+        if output is None or output.dtype != torch.float16 or not output.is_contiguous():
+            output = torch.empty((m, self.width), dtype=torch.float16, device=self.device)
+        if bias is not None:
+            bias = bias.to(torch.float16).contiguous()
+        ws = self.cache.workspace
+        lib = _lib.load()
+        status = lib.dw4_gemm_path(
+            self._path(m) if path is None else path, self.tuning_params.PREFILL_SPLIT_K,
+            m, self.height, self.width, self.group_size,
+            x2.data_ptr(), x2.stride(0),
+            self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
+            _ptr(self.perm) if self.use_act else None, _ptr(bias),
+            output.data_ptr(), output.stride(0) if output.dim() == 2 else self.width,
+            ws.data_ptr(), ws.numel(), _stream(self.device))
+        _lib.check("dw4_gemm_path", status)
+        out = output.view(outshape)
+        return out if in_dtype == torch.float16 else out.to(in_dtype)
+
+    def get_float16_weights_matrix_v2(self, out_matrix: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Dequantised fp16 weight [K, N] in the checkpoint's row order."""
+        if out_matrix is None:
+            out_matrix = torch.empty(self.height, self.width, dtype=torch.float16, device=self.device)
+        if out_matrix.dtype != torch.float16 or tuple(out_matrix.shape[-2:]) != (self.height, self.width):
+            raise ValueError("out_matrix must be fp16 [K, N]")
+        w = out_matrix.view(self.height, self.width)
+        _lib.call("dw4_dequant", self.height, self.width, self.group_size,
+                  self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
+                  _ptr(self.perm) if self.use_act else None,
+                  w.data_ptr(), w.stride(0), _stream(self.device))
+        return out_matrix
+
+    def reconstruct_weight(self, dtype: torch.dtype = torch.float16) -> None:
+        if dtype != torch.float16:
+            raise ValueError("only fp16 reconstruction is supported")
+        self.reconstructed_weight_float16 = self.get_float16_weights_matrix_v2()
+
+    def release_weight(self, dtype: Optional[torch.dtype] = None) -> None:
+        self.reconstructed_weight_float16 = None
+
+    def transpose_matmul(self, x: torch.Tensor, weight: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``x @ W.T`` for x [..., N] (the activation gradient of the forward).
+
+        The weight is dequantised bit-exactly by the HIP kernel (into the
+        shared temp buffer unless a cached weight is given); the dense
+        product is a plain library GEMM.
+        """
+        if weight is None:
+            weight = self.reconstructed_weight_float16
+        if weight is None:
+            weight = self.cache.temp_weight.view(-1)[: self.height * self.width].view(
+                self.height, self.width)
+            self.get_float16_weights_matrix_v2(weight)
+        in_dtype = x.dtype
+        out = torch.matmul(x.to(torch.float16), weight.t())
+        return out if in_dtype == torch.float16 else out.to(in_dtype)
+
+
+class Q4LinearFunction(Function):
+    """Frozen quantised weight; only the activation receives a gradient."""
+
+    @staticmethod
+    def forward(ctx: Any, input: torch.Tensor, weight_q4: Q4MatrixV2,  # type: ignore[override]
+                bias: Optional[torch.Tensor], cache_weight: bool) -> torch.Tensor:
+        ctx.weight_q4 = weight_q4
+        cached = None
+        if cache_weight and weight_q4.reconstructed_weight_float16 is None:
+            cached = weight_q4.get_float16_weights_matrix_v2()
+        output = weight_q4.matmul(input, bias=bias)
+        if cached is not None:
+            ctx.save_for_backward(cached)
+        ctx.has_cached = cached is not None
+        return output
+
+    @staticmethod
+    def backward(ctx: Any, grad_output: torch.Tensor):  # type: ignore[override]
+        grad_input = None
+        if ctx.needs_input_grad[0]:
+            weight = ctx.saved_tensors[0] if ctx.has_cached else None
+            grad_input = ctx.weight_q4.transpose_matmul(grad_output, weight)
+        return grad_input, None, None, None
+
+
+class Q4ForwardOnlyLinearFunction(Function):
+    @staticmethod
+    def forward(ctx: Any, input: torch.Tensor, weight_q4: Q4MatrixV2,  # type: ignore[override]
+                bias: Optional[torch.Tensor]) -> torch.Tensor:
+        return weight_q4.matmul(input, bias=bias)
+
+    @staticmethod
+    def backward(ctx: Any, grad_output: torch.Tensor):  # type: ignore[override]
+        return None, None, None

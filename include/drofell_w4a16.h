@@ -1,0 +1,147 @@
+/*
+ * drofell_w4a16.h -- C ABI of the MI355X (gfx950) GPTQ int4-weight /
+ * fp16-activation quantized-Linear library (libdrofell_w4a16.so).
+ *
+ * Reference interfaces replaced (paths relative to
+ * /root/reference/After-Revision-DROFELL):
+ *   dw4_make_perm    host half of make_sequential
+ *                    (cuda_extends/exllama/q4_matrix.cu:125-159) and the
+ *                    argsort in MarlinQ4Matrix (cuda_extends/marlin.py:218-220)
+ *   dw4_repack       make_q4 (cuda_extends/exllama/entry.cpp:18-62 ->
+ *                    q4_matrix.cu:33-76 shuffle/make_sequential) and
+ *                    gptq_marlin_repack (cuda_extends/vllm/ops_registration.cpp:40-42)
+ *   dw4_gemm         q4_matmul_cuda_v2 (entry.cpp:221-251) and
+ *                    q4_matmul_blas_v2 (entry.cpp:303-340), marlin_gemm
+ *                    (ops_registration.cpp:43-49); the M-based dispatch of
+ *                    Q4MatrixV2.matmul (cuda_extends/exllama.py:492-526)
+ *   dw4_dequant      q4_to_half_matrix_v2 (entry.cpp:79-91) and
+ *                    marlin_dequant_into (cuda_extends/marlin/marlin_dequant.cu:97-172)
+ *
+ * Conventions
+ *   - Every function returns an int status (DW4_OK == 0); no exception or
+ *     abort crosses the ABI.  dw4_strerror() names a status.
+ *   - Every buffer is owned by the caller.  The library allocates nothing
+ *     on the device, keeps no pointer after a call returns and holds no
+ *     global mutable state except a per-device property cache.
+ *   - Device pointers refer to memory of the current HIP device; `stream`
+ *     is a hipStream_t (NULL = the null stream).  Work is enqueued on it.
+ *   - dw4_gemm never synchronises, never allocates and launches a fixed
+ *     sequence of kernels for a given (m, k, n, workspace) so it may be
+ *     captured into a HIP graph.  Its result is deterministic (no atomics).
+ *   - dw4_make_perm runs on the host; dw4_repack may be called once per
+ *     load or swap-in and does not synchronise either.
+ *
+ * Shapes (GPTQ checkpoint format, the module buffers of QuantLinear,
+ * operators/core/linear/real_quant.py:10-49 in the reference):
+ *   qweight int32 [K/8, N]   row k of column n at bits 4*(k%8) of word [k/8][n]
+ *   qzeros  int32 [G, N/8]   stored zero of column n at bits 4*(n%8); the
+ *                            effective zero is stored + 1
+ *   scales  fp16  [G, N]
+ *   g_idx   int32 [K]        group of each row (act-order only)
+ *   x fp16 [M, K] (row stride ldx), y fp16 [M, N] (row stride ldy)
+ *   G = K / group_size.
+ * Supported: K % 128 == 0, N % 16 == 0, group_size % 32 == 0 (or
+ * group_size == K), K % group_size == 0; act-order requires every group to
+ * hold exactly group_size rows (what GPTQ desc_act produces).
+ *
+ * Packed layout written by dw4_repack (same byte counts as the inputs, so
+ * a module keeps its buffer sizes):
+ *   packed_qweight  K*N/2 bytes.  Strip s = 16 columns, chunk c = 128
+ *                   (sorted) rows; chunk (s, c) is 1024 contiguous bytes at
+ *                   (s*K/128 + c)*1024.  Lane L in [0,64), word w in [0,4)
+ *                   at byte L*16 + w*4 holds column 16*s + L%16, rows
+ *                   128*c + 32*w + 8*(L/16) + e, e in [0,8); even e at bits
+ *                   4*(e/2), odd e at bits 16 + 4*(e/2).
+ *   packed_scales   fp16, element (s, g, j) at (s*G + g)*16 + j.
+ *   packed_zeros    int32, word (s, g, h) at (s*G + g)*2 + h = qzeros[g][2s+h].
+ *   perm            int32 [K] sorted row -> original row (act-order only).
+ */
+#ifndef DROFELL_W4A16_H
+#define DROFELL_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DW4_ABI_VERSION 1
+
+enum {
+  DW4_OK = 0,
+  DW4_ERR_INVALID_ARG = 1,   /* null pointer, non-positive size, bad stride */
+  DW4_ERR_UNSUPPORTED = 2,   /* shape/group size outside the supported set */
+  DW4_ERR_MISALIGNED = 3,    /* pointer or stride not 16-byte aligned */
+  DW4_ERR_BAD_GIDX = 4,      /* g_idx out of range or groups not uniform */
+  DW4_ERR_WORKSPACE = 5,     /* workspace smaller than dw4_workspace_size() */
+  DW4_ERR_LAUNCH = 6,        /* a kernel launch failed (hipGetLastError) */
+  DW4_ERR_DEVICE = 7         /* no usable HIP device / runtime error */
+};
+
+/* Path selection for dw4_gemm_path(). */
+enum {
+  DW4_PATH_AUTO = 0,
+  DW4_PATH_DECODE = 1,   /* register-dequant MFMA kernel, M <= 64 */
+  DW4_PATH_PREFILL = 2   /* LDS-staged MFMA kernel, any M */
+};
+
+int dw4_abi_version(void);
+const char* dw4_strerror(int status);
+
+/* Byte sizes of the repacked buffers and the dw4_gemm workspace needed for
+ * any M <= max_m.  Any output pointer may be NULL. */
+int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
+                    size_t* packed_qweight_bytes, size_t* packed_scales_bytes,
+                    size_t* packed_zeros_bytes, size_t* perm_bytes,
+                    size_t* workspace_bytes);
+
+/* Workspace bytes one dw4_gemm call at exactly this M needs (0 allowed when
+ * it returns 0). */
+int dw4_workspace_size(int m, int k, int n, int group_size, int act_order,
+                       size_t* workspace_bytes);
+
+/* Host: stable counting sort of rows by group (perm[new] = old) and its
+ * validation.  g_idx_host, perm_host: int32 [k] host arrays. */
+int dw4_make_perm(int k, int group_size, const int32_t* g_idx_host,
+                  int32_t* perm_host);
+
+/* Device: GPTQ buffers -> packed layout.  perm (device int32 [k]) is NULL
+ * for checkpoints without act-order.  Outputs must not alias inputs. */
+int dw4_repack(int k, int n, int group_size,
+               const int32_t* qweight, const int32_t* qzeros,
+               const uint16_t* scales, const int32_t* perm,
+               int32_t* packed_qweight, int32_t* packed_zeros,
+               uint16_t* packed_scales, void* stream);
+
+/* Device: y[M, N] = x[M, K] @ W (+ bias[N] in fp16), fp32 accumulation,
+ * fp16 output (round to nearest even).  perm as in dw4_repack; bias may be
+ * NULL.  x and y must be 16-byte aligned with ldx % 8 == 0. */
+int dw4_gemm(int m, int k, int n, int group_size,
+             const uint16_t* x, int64_t ldx,
+             const int32_t* packed_qweight, const int32_t* packed_zeros,
+             const uint16_t* packed_scales, const int32_t* perm,
+             const uint16_t* bias, uint16_t* y, int64_t ldy,
+             void* workspace, size_t workspace_bytes, void* stream);
+
+/* dw4_gemm with an explicit path (DW4_PATH_*) and prefill split-K factor
+ * (0 = automatic); for tests and benchmarks. */
+int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size,
+                  const uint16_t* x, int64_t ldx,
+                  const int32_t* packed_qweight, const int32_t* packed_zeros,
+                  const uint16_t* packed_scales, const int32_t* perm,
+                  const uint16_t* bias, uint16_t* y, int64_t ldy,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device: dequantised fp16 weight w[K, N] (row stride ldw) in ORIGINAL row
+ * order, bit-exact with fp16_rne(scale * (q - (zero + 1))). */
+int dw4_dequant(int k, int n, int group_size,
+                const int32_t* packed_qweight, const int32_t* packed_zeros,
+                const uint16_t* packed_scales, const int32_t* perm,
+                uint16_t* w, int64_t ldw, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DROFELL_W4A16_H */

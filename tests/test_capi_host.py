@@ -1,0 +1,172 @@
+"""CPU tests: the C-ABI library loads and exports what the header declares,
+its host-only entry points behave, and the Python operator layer keeps the
+reference's quantized-Linear interface.  No test here launches a kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from gptq_synth import LLAMA2_7B_SHAPES, algorithmic_bytes, make_layer
+from hip_extends import _lib
+from oracle import gptq
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "drofell_w4a16.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(dw4_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) == 9, names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert lib.dw4_abi_version() == 1
+
+
+def test_strerror_names_every_status():
+    msgs = {s: _lib.strerror(s) for s in range(8)}
+    assert msgs[0] == "ok"
+    assert len(set(msgs.values())) == 8
+    assert _lib.strerror(99) == "unknown status"
+
+
+def test_query_sizes_preserve_checkpoint_bytes():
+    for k, n in set(LLAMA2_7B_SHAPES.values()):
+        sizes = _lib.query_sizes(k, n, 128, False, 4096)
+        assert sizes["packed_qweight"] == k * n // 2          # == qweight numel * 4
+        assert sizes["packed_scales"] == (k // 128) * n * 2   # == scales bytes
+        assert sizes["packed_zeros"] == (k // 128) * n // 2   # == qzeros bytes
+        assert sizes["perm"] == 0
+    act = _lib.query_sizes(5120, 13824, 128, True, 64)
+    assert act["perm"] == 5120 * 4
+    assert act["workspace"] >= 64 * 5120 * 2  # act-order decode gather buffer
+
+
+def test_shape_validation_codes():
+    lib = _lib.load()
+    st = lib.dw4_query_sizes(100, 4096, 128, 0, 1, None, None, None, None, None)
+    assert st == _lib.DW4_ERR_UNSUPPORTED
+    st = lib.dw4_query_sizes(4096, 4096, 48, 0, 1, None, None, None, None, None)
+    assert st == _lib.DW4_ERR_UNSUPPORTED
+    st = lib.dw4_query_sizes(0, 4096, 128, 0, 1, None, None, None, None, None)
+    assert st == _lib.DW4_ERR_INVALID_ARG
+    # gemm / repack / dequant reject before touching a device
+    assert lib.dw4_gemm(1, 96, 64, 32, None, 96, None, None, None, None, None, None, 64,
+                        None, 0, None) == _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_gemm(1, 128, 64, 128, None, 128, None, None, None, None, None, None, 64,
+                        None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_gemm(0, 128, 64, 128, None, 128, None, None, None, None, None, None, 64,
+                        None, 0, None) == _lib.DW4_OK  # empty input: nothing to do
+    assert lib.dw4_repack(128, 64, 128, None, None, None, None, None, None, None,
+                          None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_dequant(128, 64, 128, None, None, None, None, None, 64,
+                           None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_gemm_path(7, 0, 1, 128, 64, 128, None, 128, None, None, None, None, None,
+                             None, 64, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("k,g", [(256, 32), (4096, 128), (13824, 128)])
+def test_make_perm_matches_oracle(k, g):
+    rng = np.random.default_rng(k)
+    g_idx = (rng.permutation(k) // g).astype(np.int32)
+    perm = np.empty(k, dtype=np.int32)
+    _lib.call("dw4_make_perm", k, g, g_idx.ctypes.data, perm.ctypes.data)
+    assert np.array_equal(perm, gptq.act_order_perm(g_idx, k // g))
+
+
+def test_make_perm_rejects_bad_g_idx():
+    lib = _lib.load()
+    perm = np.empty(256, dtype=np.int32)
+    uneven = np.concatenate([np.zeros(100), np.ones(156)]).astype(np.int32)
+    assert lib.dw4_make_perm(256, 128, uneven.ctypes.data, perm.ctypes.data) == _lib.DW4_ERR_BAD_GIDX
+    out_of_range = (np.arange(256) // 64).astype(np.int32)
+    assert lib.dw4_make_perm(256, 128, out_of_range.ctypes.data,
+                             perm.ctypes.data) == _lib.DW4_ERR_BAD_GIDX
+    ident = (np.arange(256) // 128).astype(np.int32)
+    assert lib.dw4_make_perm(256, 128, ident.ctypes.data, perm.ctypes.data) == _lib.DW4_OK
+    assert np.array_equal(perm, np.arange(256))
+
+
+def test_workspace_size_rules():
+    assert _lib.workspace_size(1, 4096, 4096, 128, False) == 0
+    assert _lib.workspace_size(8, 4096, 4096, 128, True) == 8 * 4096 * 2
+    ws = _lib.workspace_size(256, 4096, 4096, 128, False)
+    assert ws % (256 * 4096 * 4) == 0  # whole fp32 split-K partial planes
+
+
+def test_quantlinear_buffers_match_reference_layout():
+    from operators.core.linear.real_quant import QuantLinear, QuantLinearMaker
+    maker = QuantLinearMaker(quantization_group_size=128, use_act_order=False)
+    lin = maker.make_linear(4096, 11008, bias=False)
+    assert tuple(lin.qweight.shape) == (512, 11008) and lin.qweight.dtype == torch.int32
+    assert tuple(lin.qzeros.shape) == (32, 1376) and lin.qzeros.dtype == torch.int32
+    assert tuple(lin.scales.shape) == (32, 11008) and lin.scales.dtype == torch.float16
+    assert tuple(lin.g_idx.shape) == (4096,) and lin.g_idx.dtype == torch.int32
+    assert torch.equal(lin.g_idx, torch.arange(4096, dtype=torch.int32) // 128)
+    assert lin.bias is None
+    assert sorted(dict(lin.named_buffers()).keys()) == ["g_idx", "qweight", "qzeros", "scales"]
+    lb = QuantLinear(-1, 256, 64, True, False)
+    assert lb.group_size == 256 and tuple(lb.bias.shape) == (64,)
+    with pytest.raises(AssertionError):
+        QuantLinear(128, 100, 64, False, False)
+    with pytest.raises(AssertionError):
+        QuantLinear(128, 256, 48, False, False)
+    # state_dict keys round-trip from a synthetic checkpoint
+    lay = make_layer(256, 64, 128, seed=1)
+    lin2 = maker.make_linear(256, 64)
+    lin2.load_state_dict({"qweight": lay.qweight, "qzeros": lay.qzeros,
+                          "scales": lay.scales, "g_idx": lay.g_idx})
+    assert torch.equal(lin2.qweight, lay.qweight)
+    with pytest.raises(RuntimeError):
+        lin2(torch.zeros(1, 256, dtype=torch.float16))  # not repacked yet
+    with pytest.raises(AssertionError):
+        lin2.post_init(None, None)  # buffers still on the CPU
+
+
+def test_maker_post_init_once():
+    from operators.core.linear.real_quant import QuantLinearMaker
+    maker = QuantLinearMaker(128, False)
+    maker.post_init(None, None)  # no linears: nothing to repack
+    with pytest.raises(AssertionError):
+        maker.post_init(None, None)
+
+
+def test_quantization_config():
+    from operators.core.linear.common import QuantizationConfig
+    QuantizationConfig(bits=4, group_size=128, desc_act=False, quant_method="gptq")
+    with pytest.raises(AssertionError):
+        QuantizationConfig(bits=8, group_size=128, desc_act=False, quant_method="gptq")
+    with pytest.raises(AssertionError):
+        QuantizationConfig(bits=4, group_size=128, desc_act=False, quant_method="awq")
+
+
+def test_algorithmic_bytes_match_baseline_table():
+    # values quoted in BASELINE.md section 3
+    assert algorithmic_bytes(1, 4096, 4096, 128, False) == 8_732_672
+    assert algorithmic_bytes(1, 4096, 4096, 128, False, count_zeros=False) == 8_667_136
+    assert algorithmic_bytes(16, 4096, 11008, 128, False) == 23_908_352
+    assert algorithmic_bytes(256, 4096, 4096, 128, False) == 12_910_592
+    assert algorithmic_bytes(1, 13824, 5120, 128, True) == 36_865_024
+    layer = sum(algorithmic_bytes(1, k, n, 128, False) for k, n in LLAMA2_7B_SHAPES.values())
+    assert layer * 8 == 842_371_072  # 8-layer M=1 rotation used by bench.py
+    layer8 = sum(algorithmic_bytes(8, k, n, 128, False) for k, n in LLAMA2_7B_SHAPES.values())
+    assert layer8 * 8 == 851_116_032  # BASELINE config 5 GEMM bytes per decode step
+
+
+def test_synthetic_act_order_groups_uniform():
+    lay = make_layer(1024, 32, 128, seed=4, act_order=True)
+    counts = torch.bincount(lay.g_idx.long(), minlength=8)
+    assert torch.all(counts == 128)
+    assert not torch.equal(lay.g_idx, torch.arange(1024, dtype=torch.int32) // 128)

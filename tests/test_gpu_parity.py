@@ -1,0 +1,288 @@
+"""GPU parity of the HIP W4A16 path against the pinned CPU oracle.
+
+Bars (BASELINE): dequantised fp16 weights bit-exact; GEMM outputs within
+max|y - y_ref| <= 2e-2 * ||y_ref row||_inf of a wide-accumulated reference.
+Every case prints its name before touching the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from gptq_synth import make_layer, make_x
+from hip_extends import _lib
+from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
+from oracle import gptq
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2  # BASELINE: max-abs error <= 2e-2 * ||row||_inf
+
+
+def say(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def build(layer, dev, max_m=4096):
+    lay = layer.to(dev)
+    cache = CacheV2(dev)
+    q4 = Q4MatrixV2(lay.qweight, lay.qzeros, lay.scales, lay.in_features, lay.out_features,
+                    lay.g_idx if lay.act_order else None, lay.act_order,
+                    TuningParams(MAX_M=max_m), cache)
+    cache.init_cache()
+    return q4
+
+
+@functools.lru_cache(maxsize=8)
+def oracle_w(k, n, g, seed, sym, act):
+    lay = make_layer(k, n, g, seed=seed, symmetric=sym, act_order=act)
+    a = lay.numpy()
+    return lay, gptq.dequantize(a["qweight"], a["qzeros"], a["scales"], a["g_idx"])
+
+
+def check_tol(y_gpu: torch.Tensor, y_ref: np.ndarray, what: str) -> float:
+    y = y_gpu.float().cpu().numpy()
+    assert np.all(np.isfinite(y)), what
+    ok, worst = gptq.within_tolerance(y, y_ref, TOL)
+    assert ok, f"{what}: worst error ratio {worst:.4f} > 1"
+    return worst
+
+
+# ---------------------------------------------------------------------------
+# bit-exact dequantisation
+# ---------------------------------------------------------------------------
+def test_golden_dequant_bit_exact(hip_device):
+    data = np.load("tests/golden/gptq_small.npz")
+    names = sorted({k.split("/")[0] for k in data.files})
+    for name in names:
+        say(f"golden dequant {name}")
+        k, n, g, sym, act, m = data[f"{name}/meta"].tolist()
+        cache = CacheV2(hip_device)
+        q4 = Q4MatrixV2(torch.from_numpy(data[f"{name}/qweight"]).to(hip_device),
+                        torch.from_numpy(data[f"{name}/qzeros"]).to(hip_device),
+                        torch.from_numpy(data[f"{name}/scales"]).to(hip_device), k, n,
+                        torch.from_numpy(data[f"{name}/g_idx"]).to(hip_device) if act else None,
+                        bool(act), TuningParams(), cache)
+        cache.init_cache()
+        w = q4.get_float16_weights_matrix_v2().cpu().numpy().view(np.uint16)
+        assert np.array_equal(w, data[f"{name}/w"]), name
+
+
+def test_dequant_exhaustive_kat(hip_device):
+    """All 16 q x 16 stored zeros x 65,536 fp16 scale patterns, bit for bit."""
+    say("exhaustive dequant KAT K=512 N=65536 g=32")
+    K, N, G = 512, 65536, 16
+    q = np.zeros((K, N), dtype=np.uint8)
+    for z in range(16):
+        for qq in range(16):
+            q[z * 32 + 2 * qq: z * 32 + 2 * qq + 2, :] = qq
+    zeros = np.repeat(np.arange(16, dtype=np.uint8)[:, None], N, axis=1)
+    srow = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    scales = np.repeat(srow[None, :], G, axis=0).view(np.float16)
+    qweight, qzeros = gptq.pack_qweight(q), gptq.pack_qzeros(zeros)
+    g_idx = (np.arange(K) // 32).astype(np.int32)
+    with np.errstate(all="ignore"):
+        ref = gptq.dequantize(qweight, qzeros, scales, g_idx)
+    cache = CacheV2(hip_device)
+    q4 = Q4MatrixV2(torch.from_numpy(qweight).to(hip_device), torch.from_numpy(qzeros).to(hip_device),
+                    torch.from_numpy(scales).to(hip_device), K, N, None, False, TuningParams(), cache)
+    w = q4.get_float16_weights_matrix_v2().cpu().numpy()
+    same = (w.view(np.uint16) == ref.view(np.uint16)) | (np.isnan(w) & np.isnan(ref))
+    assert same.all(), np.argwhere(~same)[:5]
+
+
+# ---------------------------------------------------------------------------
+# GEMM parity
+# ---------------------------------------------------------------------------
+def test_golden_gemm(hip_device):
+    data = np.load("tests/golden/gptq_small.npz")
+    names = sorted({k.split("/")[0] for k in data.files})
+    for name in names:
+        k, n, g, sym, act, m = data[f"{name}/meta"].tolist()
+        cache = CacheV2(hip_device)
+        q4 = Q4MatrixV2(torch.from_numpy(data[f"{name}/qweight"]).to(hip_device),
+                        torch.from_numpy(data[f"{name}/qzeros"]).to(hip_device),
+                        torch.from_numpy(data[f"{name}/scales"]).to(hip_device), k, n,
+                        torch.from_numpy(data[f"{name}/g_idx"]).to(hip_device) if act else None,
+                        bool(act), TuningParams(), cache)
+        cache.init_cache()
+        x = torch.from_numpy(data[f"{name}/x"]).to(hip_device)
+        bias = data[f"{name}/bias"] if f"{name}/bias" in data.files else None
+        bt = torch.from_numpy(bias).to(hip_device) if bias is not None else None
+        # reference value (wide accumulation) for the tolerance check
+        w = data[f"{name}/w"].view(np.float16)
+        y_ref = gptq.gemm_ref(data[f"{name}/x"], w)
+        if bias is not None:
+            y_ref = y_ref + bias.astype(np.float64)[None, :]
+        paths = [_lib.DW4_PATH_AUTO, _lib.DW4_PATH_PREFILL]
+        if m <= 64:
+            paths.append(_lib.DW4_PATH_DECODE)
+        for path in paths:
+            say(f"golden gemm {name} path={path}")
+            y = q4.matmul(x, bias=bt, path=path)
+            torch.cuda.synchronize()
+            check_tol(y, y_ref, f"{name} path {path}")
+            fix = data[f"{name}/y"].view(np.float16).astype(np.float64)
+            assert np.max(np.abs(y.float().cpu().numpy() - fix)) <= \
+                np.max(np.abs(fix)) * 4e-3 + 1e-3, name
+
+
+SHAPES_7B = [(4096, 4096), (4096, 11008), (11008, 4096)]
+
+
+@pytest.mark.parametrize("kn", SHAPES_7B, ids=lambda kn: f"{kn[0]}x{kn[1]}")
+def test_decode_7b_shapes(hip_device, kn):
+    k, n = kn
+    lay, w = oracle_w(k, n, 128, 1000 + SHAPES_7B.index(kn), False, False)
+    q4 = build(lay, hip_device)
+    for m in (1, 2, 4, 8, 16, 33, 64):
+        say(f"decode 7B {k}x{n} M={m}")
+        x = make_x(m, k, seed=m)
+        y = q4.matmul(x.to(hip_device), path=_lib.DW4_PATH_DECODE)
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"decode {k}x{n} M={m}")
+
+
+@pytest.mark.parametrize("kn", SHAPES_7B, ids=lambda kn: f"{kn[0]}x{kn[1]}")
+def test_prefill_7b_shapes(hip_device, kn):
+    k, n = kn
+    lay, w = oracle_w(k, n, 128, 1000 + SHAPES_7B.index(kn), False, False)
+    q4 = build(lay, hip_device)
+    for m in (16, 64, 100, 256):
+        say(f"prefill 7B {k}x{n} M={m}")
+        x = make_x(m, k, seed=m + 7)
+        y = q4.matmul(x.to(hip_device), path=_lib.DW4_PATH_PREFILL)
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"prefill {k}x{n} M={m}")
+
+
+def test_symmetric_c1(hip_device):
+    lay, w = oracle_w(4096, 4096, 128, 0, True, False)
+    q4 = build(lay, hip_device)
+    say("C1 symmetric 4096x4096 M=1")
+    x = make_x(1, 4096, seed=0)
+    y = q4.matmul(x.to(hip_device))
+    torch.cuda.synchronize()
+    check_tol(y, gptq.gemm_ref(x.numpy(), w), "C1")
+
+
+@pytest.mark.parametrize("kn", [(5120, 5120), (13824, 5120), (5120, 13824)],
+                         ids=lambda kn: f"{kn[0]}x{kn[1]}")
+def test_act_order_13b(hip_device, kn):
+    k, n = kn
+    lay, w = oracle_w(k, n, 128, 2000 + k + n, False, True)
+    q4 = build(lay, hip_device)
+    assert q4.use_act
+    for m in (1, 8, 64):
+        for path in (_lib.DW4_PATH_DECODE, _lib.DW4_PATH_PREFILL):
+            say(f"act-order 13B {k}x{n} M={m} path={path}")
+            x = make_x(m, k, seed=m + 11)
+            y = q4.matmul(x.to(hip_device), path=path)
+            torch.cuda.synchronize()
+            check_tol(y, gptq.gemm_ref(x.numpy(), w), f"act {k}x{n} M={m} path {path}")
+
+
+@pytest.mark.parametrize("g", [32, 64, 256, 1024])
+def test_group_sizes(hip_device, g):
+    k, n = 1024, 272  # N = 17 strips: a partial prefill N-tile
+    for act in (False, True):
+        lay, w = oracle_w(k, n, g, 3000 + g, False, act)
+        q4 = build(lay, hip_device)
+        for m in (1, 5, 33, 100):
+            for path in ((_lib.DW4_PATH_DECODE, _lib.DW4_PATH_PREFILL) if m <= 64
+                         else (_lib.DW4_PATH_PREFILL,)):
+                say(f"group g={g} act={act} M={m} path={path}")
+                x = make_x(m, k, seed=m + g)
+                y = q4.matmul(x.to(hip_device), path=path)
+                torch.cuda.synchronize()
+                check_tol(y, gptq.gemm_ref(x.numpy(), w), f"g={g} act={act} M={m} path {path}")
+        # dequantised weight bit-exact for every group size / act-order
+        say(f"group g={g} act={act} dequant")
+        wd = q4.get_float16_weights_matrix_v2().cpu().numpy()
+        assert np.array_equal(wd.view(np.uint16), w.view(np.uint16))
+
+
+def test_prefill_large_m_and_split_k(hip_device):
+    lay, w = oracle_w(4096, 4096, 128, 1000, False, False)
+    q4 = build(lay, hip_device)
+    x = make_x(2048, 4096, seed=2048)
+    ref = gptq.gemm_ref(x.numpy(), w)
+    xd = x.to(hip_device)
+    for split in (0, 1, 3, 8):
+        say(f"prefill M=2048 split={split}")
+        q4.tuning_params = TuningParams(PREFILL_SPLIT_K=split)
+        y = q4.matmul(xd, path=_lib.DW4_PATH_PREFILL)
+        torch.cuda.synchronize()
+        check_tol(y, ref, f"M=2048 split {split}")
+
+
+def test_deterministic(hip_device):
+    lay, _ = oracle_w(4096, 11008, 128, 1001, False, False)
+    q4 = build(lay, hip_device)
+    for m, path in ((1, _lib.DW4_PATH_DECODE), (16, _lib.DW4_PATH_DECODE),
+                    (64, _lib.DW4_PATH_PREFILL), (256, _lib.DW4_PATH_PREFILL)):
+        say(f"determinism M={m} path={path}")
+        x = make_x(m, 4096, seed=99).to(hip_device)
+        outs = [q4.matmul(x, path=path).clone() for _ in range(3)]
+        torch.cuda.synchronize()
+        for o in outs[1:]:
+            assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
+def test_graph_capture_replay(hip_device):
+    lay, w = oracle_w(4096, 4096, 128, 1000, False, False)
+    q4 = build(lay, hip_device)
+    for m in (1, 8, 256):
+        say(f"graph capture M={m}")
+        x = make_x(m, 4096, seed=5).to(hip_device)
+        out = torch.empty(m, 4096, dtype=torch.float16, device=hip_device)
+        eager = q4.matmul(x).clone()
+        s = torch.cuda.Stream(device=hip_device)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            q4.matmul(x, output=out)  # warm-up outside capture
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            q4.matmul(x, output=out)
+        for rep in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), rep
+            _ = (x * 2).sum().item()  # eager work between replays
+
+
+def test_errors_surface(hip_device):
+    lay, _ = oracle_w(4096, 4096, 128, 1000, False, False)
+    q4 = build(lay, hip_device)
+    lib = _lib.load()
+    x = torch.zeros(2, 4096 + 8, dtype=torch.float16, device=hip_device)
+    y = torch.empty(1, 4096, dtype=torch.float16, device=hip_device)
+    say("errors: misaligned x pointer")
+    st = lib.dw4_gemm(1, 4096, 4096, 128, x.data_ptr() + 2, 4096, q4.qweight.data_ptr(),
+                      q4.qzeros.data_ptr(), q4.scales.data_ptr(), None, None, y.data_ptr(), 4096,
+                      None, 0, None)
+    assert st == _lib.DW4_ERR_MISALIGNED
+    say("errors: unsupported K")
+    st = lib.dw4_gemm(1, 96, 4096, 32, x.data_ptr(), 96, q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
+                      q4.scales.data_ptr(), None, None, y.data_ptr(), 4096, None, 0, None)
+    assert st == _lib.DW4_ERR_UNSUPPORTED
+    say("errors: act-order decode without workspace")
+    perm = torch.arange(4096, dtype=torch.int32, device=hip_device)
+    st = lib.dw4_gemm(1, 4096, 4096, 128, x.data_ptr(), 4096, q4.qweight.data_ptr(),
+                      q4.qzeros.data_ptr(), q4.scales.data_ptr(), perm.data_ptr(), None,
+                      y.data_ptr(), 4096, None, 0, None)
+    assert st == _lib.DW4_ERR_WORKSPACE
+    say("errors: misaligned view goes through an aligned copy")
+    xv = x[:, 1:4097]
+    out = q4.matmul(xv)
+    ref = q4.matmul(xv.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
