@@ -37,7 +37,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int check_shape(int k, int n, int group_size) {
   if (k <= 0 || n <= 0 || group_size <= 0) return DW4_ERR_INVALID_ARG;
   if (k % kChunkK != 0 || n % kStripN != 0) return DW4_ERR_UNSUPPORTED;
-  if (group_size % 32 != 0 || k % group_size != 0) return DW4_ERR_UNSUPPORTED;
+  // a 128-row chunk holds whole groups (32, 64) or lies inside one group
+  const bool small = group_size == 32 || group_size == 64;
+  if ((!small && group_size % kChunkK != 0) || k % group_size != 0) return DW4_ERR_UNSUPPORTED;
   return DW4_OK;
 }
 
@@ -73,12 +75,15 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
 bool use_decode(int path, int m) {
   if (path == DW4_PATH_DECODE) return true;
   if (path == DW4_PATH_PREFILL) return false;
-  return m <= dw4::kDecodeMaxM;
+  return m <= dw4::kDecodeAutoMaxM;
 }
 
-size_t workspace_for(int path, int m, int k, int n, int act_order) {
+size_t workspace_for(int path, int m, int k, int n, int group_size) {
   if (m <= 0) return 0;
-  if (use_decode(path, m)) return act_order ? (size_t)m * k * sizeof(uint16_t) : 0;
+  if (use_decode(path, m)) {
+    const dw4::DecodePlan p = dw4::plan_decode(m, k, group_size);
+    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+  }
   const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
   return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
 }
@@ -93,7 +98,7 @@ const char* dw4_strerror(int status) {
   switch (status) {
     case DW4_OK: return "ok";
     case DW4_ERR_INVALID_ARG: return "invalid argument (null pointer, non-positive size or bad stride)";
-    case DW4_ERR_UNSUPPORTED: return "unsupported shape: need K % 128 == 0, N % 16 == 0, group_size % 32 == 0 and K % group_size == 0";
+    case DW4_ERR_UNSUPPORTED: return "unsupported shape: need K % 128 == 0, N % 16 == 0, group_size in {32, 64} or a multiple of 128, and K % group_size == 0";
     case DW4_ERR_MISALIGNED: return "misaligned buffer: pointers must be 16-byte aligned and ldx a multiple of 8";
     case DW4_ERR_BAD_GIDX: return "g_idx out of range or groups not of uniform size group_size";
     case DW4_ERR_WORKSPACE: return "workspace too small for this call (see dw4_workspace_size)";
@@ -116,8 +121,11 @@ int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
   if (perm_bytes) *perm_bytes = act_order ? (size_t)k * sizeof(int32_t) : 0;
   if (workspace_bytes) {
     size_t ws = 0;
-    for (int m = 1; m <= max_m; ++m)
-      ws = std::max(ws, workspace_for(DW4_PATH_AUTO, m, k, n, act_order));
+    // enough for either explicit path at every M up to max_m
+    for (int m = 1; m <= max_m; ++m) {
+      ws = std::max(ws, workspace_for(DW4_PATH_PREFILL, m, k, n, group_size));
+      if (m <= dw4::kDecodeMaxM) ws = std::max(ws, workspace_for(DW4_PATH_DECODE, m, k, n, group_size));
+    }
     *workspace_bytes = ws;
   }
   return DW4_OK;
@@ -127,7 +135,8 @@ int dw4_workspace_size(int m, int k, int n, int group_size, int act_order, size_
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;
   if (m < 0 || workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
-  *workspace_bytes = workspace_for(DW4_PATH_AUTO, m, k, n, act_order);
+  (void)act_order;  // act-order gathers during staging: no extra workspace
+  *workspace_bytes = workspace_for(DW4_PATH_AUTO, m, k, n, group_size);
   return DW4_OK;
 }
 
@@ -202,18 +211,15 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
   a.ldy = ldy;
 
   if (decode) {
-    if (perm != nullptr) {
-      const size_t need = (size_t)m * k * sizeof(uint16_t);
+    const dw4::DecodePlan plan = dw4::plan_decode(m, k, group_size);
+    float* part = nullptr;
+    if (plan.splits > 1) {
+      const size_t need = (size_t)plan.splits * m * n * sizeof(float);
       if (workspace == nullptr || workspace_bytes < need) return DW4_ERR_WORKSPACE;
       if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
-      uint16_t* xg = static_cast<uint16_t*>(workspace);
-      hipError_t e = dw4::launch_gather_x(x, ldx, perm, xg, m, k, s);
-      if (e != hipSuccess) return DW4_ERR_LAUNCH;
-      a.x = xg;
-      a.ldx = k;
-      a.perm = nullptr;
+      part = static_cast<float*>(workspace);
     }
-    return status_of(dw4::launch_decode(a, s));
+    return status_of(dw4::launch_decode(a, plan, part, s));
   }
 
   dw4::PrefillPlan plan = plan_prefill(m, k, n, split_k, workspace ? workspace_bytes : 0, true);

@@ -119,159 +119,228 @@ __global__ void repack_meta_kernel(const uint16_t* __restrict__ scales,
 }
 
 // ---------------------------------------------------------------------------
-// Act-order activation gather for the decode path: xg[m][k'] = x[m][perm[k']]
+// Per-(strip, group) metadata record as staged in LDS: 8 dwords holding the
+// 16 fp16 scales of the strip's columns, then the 2 dwords of stored zeros.
 // ---------------------------------------------------------------------------
-__global__ void gather_x_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                const int32_t* __restrict__ perm,
-                                uint16_t* __restrict__ xg, int M, int K) {
-  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= (size_t)M * K) return;
-  const int m = (int)(o / K);
-  const int k = (int)(o % K);
-  xg[o] = x[(size_t)m * ldx + perm[k]];
+constexpr int kMetaWords = 10;
+
+__device__ __forceinline__ uint32_t meta_word(const uint32_t* __restrict__ ps32,
+                                              const uint32_t* __restrict__ pz, int G, int strip,
+                                              int g, int w) {
+  const size_t sg = (size_t)strip * G + g;
+  return w < 8 ? ps32[sg * 8 + w] : pz[sg * 2 + (w - 8)];
+}
+
+// One 16-byte unit (8 consecutive sorted rows) of an activation row,
+// gathered through perm for act-order checkpoints.
+template <bool ACT>
+__device__ __forceinline__ h8 load_x_unit(const _Float16* __restrict__ row,
+                                          const int32_t* __restrict__ perm, int k) {
+  if (ACT) {
+    const i4 p0 = *(const i4*)(perm + k);
+    const i4 p1 = *(const i4*)(perm + k + 4);
+    return h8{row[p0[0]], row[p0[1]], row[p0[2]], row[p0[3]],
+              row[p1[0]], row[p1[1]], row[p1[2]], row[p1[3]]};
+  }
+  return *(const h8*)(row + k);
 }
 
 // ---------------------------------------------------------------------------
-// Decode kernel (M <= 64): one workgroup per 16-column strip, its waves
-// split K; packed int4 words are dequantised in registers straight into the
-// B operand of v_mfma_f32_16x16x32_f16 (no LDS for weights); the scale is
-// applied per group in fp32; the waves' partial sums meet in LDS in a fixed
-// order (deterministic).
+// Decode kernel (M <= 64).  Grid: (N/16 strips) x (K splits).  The
+// workgroup first stages its activation slice (gathered for act-order) and
+// the strip's scales/zeros for its K range in LDS, while the packed weight
+// words stream into a U-deep register ring (non-temporal 16-byte loads,
+// 1 KB contiguous per wave).  Its waves take interleaved 128-row chunks;
+// each word is dequantised in registers straight into the B operand of
+// v_mfma_f32_16x16x32_f16 (exact q - z in fp16), the scale is applied per
+// group in fp32, and the waves' partial sums meet in LDS in a fixed order.
+// The only global loads inside the main loop are the weight ring's, so no
+// wait in the loop covers more than the oldest ring slot.
 // ---------------------------------------------------------------------------
-template <int MT, int WAVES, int U, bool G128>
+constexpr int kXBatch = 4;  // activation units per thread per staging pass
+constexpr int kMBatch = 4;  // metadata dwords per thread per staging pass
+
+template <int MT, int WAVES, int U, bool G128, bool ACT>
 __global__ void __launch_bounds__(WAVES * 64)
-decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
+decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ perm,
               const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
-              const uint16_t* __restrict__ ps, const uint16_t* __restrict__ bias,
-              uint16_t* __restrict__ y, int64_t ldy, int K, int gs, int G) {
-  __shared__ __attribute__((aligned(16))) f4 red[WAVES * MT * 64];
+              const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
+              uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part, int K, int N,
+              int gs, int G, int cps) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int T = WAVES * 64;
   const int s = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int split = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int j = lane & 15;
   const int kq = lane >> 4;
   const int KC = K / kChunkK;
+  const int c0 = split * cps;
+  const int nc = min(KC, c0 + cps) - c0;
+  const int kr = nc * kChunkK;
+  const int ldl = kr + 8;  // halfs per staged row: 16-byte pad against bank conflicts
+  const int g0 = (c0 * kChunkK) / gs;
+  const int ng = ((c0 + nc) * kChunkK - 1) / gs - g0 + 1;
+  _Float16* xs = reinterpret_cast<_Float16*>(smem);
+  uint32_t* ms = reinterpret_cast<uint32_t*>(smem + (size_t)M * ldl * 2);
 
-  const u4* qp = pq + (size_t)s * KC * 64 + lane;
-  const uint16_t* sp = ps + (size_t)s * G * 16 + j;
-  const uint32_t* zp = pz + (size_t)s * G * 2 + (j >> 3);
+  const int xrow_units = kr >> 3;
+  const int xunits = M * xrow_units;
+  const int munits = ng * kMetaWords;
+  const int kbase = c0 * kChunkK;
+
+  // staging pass 0: issued before the weight ring so the wait for it does
+  // not cover the ring's loads
+  h8 xv[kXBatch];
+  uint32_t mv[kMBatch];
+#pragma unroll
+  for (int b = 0; b < kXBatch; ++b) {
+    const int u = tid + b * T;
+    if (u < xunits) {
+      const int m = u / xrow_units;
+      xv[b] = load_x_unit<ACT>(x + (size_t)m * ldx, perm, kbase + (u - m * xrow_units) * 8);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kMBatch; ++b) {
+    const int v = tid + b * T;
+    if (v < munits) mv[b] = meta_word(ps32, pz, G, s, g0 + v / kMetaWords, v % kMetaWords);
+  }
+
+  // weight ring
+  const u4* qp = pq + ((size_t)s * KC + c0) * 64 + lane;
+  const int nch = wave < nc ? (nc - wave + WAVES - 1) / WAVES : 0;
+  u4 qb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (u < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + u * WAVES) * 64);
+
+#pragma unroll
+  for (int b = 0; b < kXBatch; ++b) {
+    const int u = tid + b * T;
+    if (u < xunits) {
+      const int m = u / xrow_units;
+      *(h8*)(xs + (size_t)m * ldl + (u - m * xrow_units) * 8) = xv[b];
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kMBatch; ++b) {
+    const int v = tid + b * T;
+    if (v < munits) ms[v] = mv[b];
+  }
+  // further passes (large M*K or many groups)
+  for (int u = tid + kXBatch * T; u < xunits; u += T) {
+    const int m = u / xrow_units;
+    const int c8 = u - m * xrow_units;
+    *(h8*)(xs + (size_t)m * ldl + c8 * 8) =
+        load_x_unit<ACT>(x + (size_t)m * ldx, perm, kbase + c8 * 8);
+  }
+  for (int v = tid + kMBatch * T; v < munits; v += T)
+    ms[v] = meta_word(ps32, pz, G, s, g0 + v / kMetaWords, v % kMetaWords);
+  __syncthreads();
+
   const int zsh = (j & 7) * 4;
-
-  const _Float16* xr[MT];
-  bool xv[MT];
+  const _Float16* xl[MT];
+  bool xok[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + j;
-    xv[mt] = m < M;
-    xr[mt] = x + (size_t)(xv[mt] ? m : 0) * ldx + kq * 8;
+    xok[mt] = m < M;
+    xl[mt] = xs + (size_t)(xok[mt] ? m : 0) * ldl + kq * 8;
   }
-
   f4 tot[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) tot[mt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const int nch = wave < KC ? (KC - wave + WAVES - 1) / WAVES : 0;
-
-  u4 qb[U];
-  uint32_t zb[U];
-  uint16_t sb[U];
+  // One chunk: 4 k-steps of 32 rows; w holds this lane's 4 packed words.
+  auto chunk = [&](const u4 w, int lc) {
+    const int kl = lc * kChunkK;
+    f4 acc[MT];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (u < nch) {
-      const int c = wave + u * WAVES;
-      qb[u] = __builtin_nontemporal_load(qp + (size_t)c * 64);
-      if (G128) {
-        const int g = (c * kChunkK) / gs;
-        sb[u] = sp[(size_t)g * 16];
-        zb[u] = zp[(size_t)g * 2];
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+    if (G128) {
+      const uint32_t* mr = ms + (((c0 + lc) * kChunkK) / gs - g0) * kMetaWords;
+      const float sc = (float)reinterpret_cast<const _Float16*>(mr)[j];
+      h2 nz1024, nz64;
+      zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const h8 b = centered8(w[t], nz1024, nz64);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const h8 a = xok[mt] ? *(const h8*)(xl[mt] + kl + 32 * t) : h8{};
+          acc[mt] = mfma16(a, b, acc[mt]);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) tot[mt] += sc * acc[mt];
+    } else {
+      // group size 32 or 64: one or two k-steps per group
+      const int spg = gs >> 5;
+      float sc = 0.f;
+      h2 nz1024, nz64;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t % spg == 0) {
+          const uint32_t* mr = ms + (((c0 + lc) * kChunkK + 32 * t) / gs - g0) * kMetaWords;
+          sc = (float)reinterpret_cast<const _Float16*>(mr)[j];
+          zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
+        }
+        const h8 b = centered8(w[t], nz1024, nz64);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const h8 a = xok[mt] ? *(const h8*)(xl[mt] + kl + 32 * t) : h8{};
+          acc[mt] = mfma16(a, b, acc[mt]);
+        }
+        if (t % spg == spg - 1) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            tot[mt] += sc * acc[mt];
+            acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
       }
     }
-  }
+  };
 
-  for (int i0 = 0; i0 < nch; i0 += U) {
+  // Steady state: every consumed slot is refilled unconditionally, so the
+  // only wait before a slot is for that slot (U - 1 newer loads pending).
+  int i0 = 0;
+  for (; i0 + 2 * U <= nch; i0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int i = i0 + u;
-      if (i < nch) {
-        const int c = wave + i * WAVES;
-        const u4 w = qb[u];
-        uint32_t zw = 0;
-        uint16_t sbits = 0;
-        if (G128) {
-          zw = zb[u];
-          sbits = sb[u];
-        }
-        const int in = i + U;
-        if (in < nch) {
-          const int cn = wave + in * WAVES;
-          qb[u] = __builtin_nontemporal_load(qp + (size_t)cn * 64);
-          if (G128) {
-            const int g = (cn * kChunkK) / gs;
-            sb[u] = sp[(size_t)g * 16];
-            zb[u] = zp[(size_t)g * 2];
-          }
-        }
-        const size_t xoff = (size_t)c * kChunkK;
-        if (G128) {
-          h2 nz1024, nz64;
-          zero_consts(zw, zsh, nz1024, nz64);
-          f4 acc[MT];
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const h8 b = centered8(w[t], nz1024, nz64);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              h8 a = h8{};
-              if (xv[mt]) a = *(const h8*)(xr[mt] + xoff + 32 * t);
-              acc[mt] = mfma16(a, b, acc[mt]);
-            }
-          }
-          const float sc = (float)as_h(sbits);
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) tot[mt] += sc * acc[mt];
-        } else {
-          // Group size a multiple of 32 that does not cover a whole chunk or
-          // is not a multiple of 128: groups change at k-step granularity.
-          f4 acc[MT];
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
-          const int spg = gs >> 5;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int ks = c * 4 + t;
-            const int g = ks / spg;
-            h2 nz1024, nz64;
-            zero_consts(zp[(size_t)g * 2], zsh, nz1024, nz64);
-            const h8 b = centered8(w[t], nz1024, nz64);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              h8 a = h8{};
-              if (xv[mt]) a = *(const h8*)(xr[mt] + xoff + 32 * t);
-              acc[mt] = mfma16(a, b, acc[mt]);
-            }
-            const bool last = (t == 3) || ((ks + 1) / spg != g);
-            if (last) {
-              const float sc = (float)as_h(sp[(size_t)g * 16]);
-#pragma unroll
-              for (int mt = 0; mt < MT; ++mt) {
-                tot[mt] += sc * acc[mt];
-                acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
-              }
-            }
-          }
-        }
-      }
+      const int lc = wave + (i0 + u) * WAVES;
+      chunk(qb[u], lc);  // consume, then refill the same registers
+      qb[u] = __builtin_nontemporal_load(qp + (size_t)(lc + U * WAVES) * 64);
     }
   }
+  // Drain: at most 2U - 1 chunks left; refills only where a chunk remains.
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = i0 + u;
+    if (i < nch) {
+      const int lc = wave + i * WAVES;
+      chunk(qb[u], lc);
+      if (i + U < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(lc + U * WAVES) * 64);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = i0 + U + u;
+    if (i < nch) chunk(qb[u], wave + i * WAVES);
+  }
 
+  __syncthreads();  // staged activations are dead; reuse LDS for the reduction
+  f4* red = reinterpret_cast<f4*>(smem);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = tot[mt];
   __syncthreads();
 
-  const float* redf = reinterpret_cast<const float*>(red);
-  for (int idx = threadIdx.x; idx < MT * 256; idx += WAVES * 64) {
+  const float* redf = reinterpret_cast<const float*>(smem);
+  const bool direct = gridDim.y == 1;
+  for (int idx = tid; idx < MT * 256; idx += T) {
     const int llo = idx & 15;
     const int r = (idx >> 4) & 3;
     const int lhi = (idx >> 6) & 3;
@@ -283,19 +352,25 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
     for (int wv = 0; wv < WAVES; ++wv) sum += redf[((wv * MT + mt) * 64 + L) * 4 + r];
     const int n = s * kStripN + llo;
-    _Float16 out = (_Float16)sum;
-    if (bias != nullptr) out = (_Float16)((float)out + (float)as_h(bias[n]));
-    y[(size_t)m * ldy + n] = h_bits(out);
+    if (direct) {
+      _Float16 out = (_Float16)sum;
+      if (bias != nullptr) out = out + as_h(bias[n]);
+      y[(size_t)m * ldy + n] = h_bits(out);
+    } else {
+      part[((size_t)split * M + m) * N + n] = sum;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Prefill kernel (any M): 4 waves; the workgroup tile is (16*MT2) rows x
-// (64*S) columns.  Activations are staged through LDS (double buffered,
-// gathered through perm for act-order); each wave owns S strips and
-// dequantises its packed words in registers to the exact fp16 weight,
-// which feeds v_mfma_f32_16x16x32_f16 directly.  Split-K partials (fp32)
-// go to the workspace and are summed in a fixed order by reduce_kernel.
+// Prefill kernel (any M): 4 waves; workgroup tile (16*MT2) rows x (64*S)
+// columns.  Per 128-row chunk the workgroup stages the activation tile
+// (gathered for act-order) and the tile's scales/zeros into double-buffered
+// LDS; each wave owns S strips, streams their packed words into registers
+// one chunk ahead and dequantises them to the exact fp16 weight
+// (fp16_rne(scale * (q - z)), as the reference's dequantiser), which feeds
+// v_mfma_f32_16x16x32_f16 directly.  Split-K partials (fp32) go to the
+// workspace and are summed in a fixed order by reduce_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kLdaPad = 8;
 constexpr int kLda = kChunkK + kLdaPad;  // halfs per LDS row (272 bytes)
@@ -305,12 +380,17 @@ __global__ void __launch_bounds__(256)
 prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                const int32_t* __restrict__ perm,
                const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
-               const uint16_t* __restrict__ ps, const uint16_t* __restrict__ bias,
+               const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
                uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
                int K, int N, int gs, int G, int chunks_per_split, int mtiles, int ntiles) {
   constexpr int BM = 16 * MT2;
-  constexpr int UNITS = BM * 16 / 256;  // 16-byte A units per thread per chunk
+  constexpr int UNITS = BM * 16 / 256;  // 16-byte activation units per thread per chunk
+  constexpr int NSTRIP = 4 * S;
+  constexpr int GPC = G128 ? 1 : 4;     // group records per strip per chunk (max)
+  constexpr int MW = NSTRIP * GPC * kMetaWords;
+  constexpr int MU = (MW + 255) / 256;  // metadata dwords per thread per chunk
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLda];
+  __shared__ __attribute__((aligned(16))) uint32_t Ms[2][MW];
 
   // XCD-aware tile order: the M-tiles of one N-tile get block ids congruent
   // modulo 8, so they run on one XCD and share its L2 copy of the weights.
@@ -331,8 +411,11 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const int c_begin = split * chunks_per_split;
   const int c_end = min(KC, c_begin + chunks_per_split);
   const int m0 = mtile * BM;
+  const int NS = N / kStripN;
+  const int gpc = G128 ? 1 : kChunkK / gs;  // 4 (gs 32) or 2 (gs 64)
+  const int strip_base = ntile * NSTRIP;
 
-  // Activation staging: unit u -> (row, 16-byte column)
+  // activation staging: unit u -> (row, 16-byte column)
   int arow[UNITS], acol[UNITS];
   bool aval[UNITS];
 #pragma unroll
@@ -344,46 +427,55 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   }
   auto load_a = [&](int c, h8 (&regs)[UNITS]) {
 #pragma unroll
-    for (int i = 0; i < UNITS; ++i) {
-      h8 v = h8{};
-      if (aval[i]) {
-        const _Float16* xrow = x + (size_t)(m0 + arow[i]) * ldx;
-        const int k = c * kChunkK + acol[i] * 8;
-        if (ACT) {
-          const i4 p0 = *(const i4*)(perm + k);
-          const i4 p1 = *(const i4*)(perm + k + 4);
-          v = h8{xrow[p0[0]], xrow[p0[1]], xrow[p0[2]], xrow[p0[3]],
-                 xrow[p1[0]], xrow[p1[1]], xrow[p1[2]], xrow[p1[3]]};
-        } else {
-          v = *(const h8*)(xrow + k);
-        }
-      }
-      regs[i] = v;
-    }
+    for (int i = 0; i < UNITS; ++i)
+      regs[i] = aval[i] ? load_x_unit<ACT>(x + (size_t)(m0 + arow[i]) * ldx, perm,
+                                           c * kChunkK + acol[i] * 8)
+                        : h8{};
   };
   auto store_a = [&](int buf, const h8 (&regs)[UNITS]) {
 #pragma unroll
-    for (int i = 0; i < UNITS; ++i)
-      *(h8*)(&As[buf][arow[i] * kLda + acol[i] * 8]) = regs[i];
+    for (int i = 0; i < UNITS; ++i) *(h8*)(&As[buf][arow[i] * kLda + acol[i] * 8]) = regs[i];
+  };
+  // metadata staging: dword v -> (local strip, group within chunk, word)
+  const int mwords = NSTRIP * gpc * kMetaWords;
+  auto load_m = [&](int c, uint32_t (&regs)[MU]) {
+#pragma unroll
+    for (int i = 0; i < MU; ++i) {
+      const int v = tid + 256 * i;
+      regs[i] = 0u;
+      if (v < mwords) {
+        const int sl = v / (gpc * kMetaWords);
+        const int rem = v - sl * gpc * kMetaWords;
+        const int gl = rem / kMetaWords;
+        const int st = strip_base + sl;
+        if (st < NS)
+          regs[i] = meta_word(ps32, pz, G, st, (c * kChunkK) / gs + gl, rem - gl * kMetaWords);
+      }
+    }
+  };
+  auto store_m = [&](int buf, const uint32_t (&regs)[MU]) {
+#pragma unroll
+    for (int i = 0; i < MU; ++i) {
+      const int v = tid + 256 * i;
+      if (v < mwords) Ms[buf][v] = regs[i];
+    }
   };
 
-  // Weight strips owned by this wave (the last N-tile may be partial).
-  const int NS = N / kStripN;
-  const int strip0 = ntile * 4 * S + wave * S;
+  // weight strips owned by this wave (the last N-tile may be partial)
+  const int strip0 = strip_base + wave * S;
   const u4* qp[S];
-  const uint16_t* sp[S];
-  const uint32_t* zp[S];
   bool sval[S];
 #pragma unroll
   for (int si = 0; si < S; ++si) {
     const int st = strip0 + si;
     sval[si] = st < NS;
-    const int sc = sval[si] ? st : 0;
-    qp[si] = pq + (size_t)sc * KC * 64 + lane;
-    sp[si] = ps + (size_t)sc * G * 16 + j;
-    zp[si] = pz + (size_t)sc * G * 2 + (j >> 3);
+    qp[si] = pq + (size_t)(sval[si] ? st : 0) * KC * 64 + lane;
   }
-  const int zsh = (j & 7) * 4;
+  auto load_b = [&](int c, u4 (&q)[S]) {
+#pragma unroll
+    for (int si = 0; si < S; ++si)
+      q[si] = sval[si] ? __builtin_nontemporal_load(qp[si] + (size_t)c * 64) : u4{0u, 0u, 0u, 0u};
+  };
 
   f4 acc[MT2][S];
 #pragma unroll
@@ -392,52 +484,39 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     for (int si = 0; si < S; ++si) acc[mt][si] = f4{0.f, 0.f, 0.f, 0.f};
 
   h8 areg[UNITS];
+  uint32_t mreg[MU];
   u4 qcur[S], qnext[S];
-  uint32_t zcur[S], znext[S];
-  uint16_t scur[S], snext[S];
-
-  auto load_b = [&](int c, u4 (&q)[S], uint32_t (&z)[S], uint16_t (&sc)[S]) {
-#pragma unroll
-    for (int si = 0; si < S; ++si) {
-      q[si] = sval[si] ? __builtin_nontemporal_load(qp[si] + (size_t)c * 64) : u4{0u, 0u, 0u, 0u};
-      if (G128) {
-        const int g = (c * kChunkK) / gs;
-        sc[si] = sp[si][(size_t)g * 16];
-        z[si] = zp[si][(size_t)g * 2];
-      }
-    }
-  };
 
   if (c_begin < c_end) {
     load_a(c_begin, areg);
-    load_b(c_begin, qcur, zcur, scur);
+    load_m(c_begin, mreg);
+    load_b(c_begin, qcur);
     store_a(0, areg);
+    store_m(0, mreg);
   }
   __syncthreads();
 
+  const int zsh = (j & 7) * 4;
   for (int c = c_begin; c < c_end; ++c) {
     const int buf = (c - c_begin) & 1;
     const bool has_next = (c + 1) < c_end;
     if (has_next) {
       load_a(c + 1, areg);
-      load_b(c + 1, qnext, znext, snext);
+      load_m(c + 1, mreg);
+      load_b(c + 1, qnext);
     }
     const _Float16* Ab = &As[buf][0];
+    const uint32_t* Mb = &Ms[buf][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      const int gl = G128 ? 0 : (32 * t) / gs;
       h8 bop[S];
 #pragma unroll
       for (int si = 0; si < S; ++si) {
+        const uint32_t* mr = Mb + ((wave * S + si) * gpc + gl) * kMetaWords;
+        const _Float16 sc = reinterpret_cast<const _Float16*>(mr)[j];
         h2 nz1024, nz64;
-        _Float16 sc;
-        if (G128) {
-          zero_consts(zcur[si], zsh, nz1024, nz64);
-          sc = as_h(scur[si]);
-        } else {
-          const int g = (c * kChunkK + 32 * t) / gs;
-          zero_consts(zp[si][(size_t)g * 2], zsh, nz1024, nz64);
-          sc = as_h(sp[si][(size_t)g * 16]);
-        }
+        zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
         const h8 d = centered8(qcur[si][t], nz1024, nz64);
         const h8 s8 = h8{sc, sc, sc, sc, sc, sc, sc, sc};
         bop[si] = d * s8;  // fp16 product, round to nearest even
@@ -451,12 +530,9 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     }
     if (has_next) {
       store_a(buf ^ 1, areg);
+      store_m(buf ^ 1, mreg);
 #pragma unroll
-      for (int si = 0; si < S; ++si) {
-        qcur[si] = qnext[si];
-        zcur[si] = znext[si];
-        scur[si] = snext[si];
-      }
+      for (int si = 0; si < S; ++si) qcur[si] = qnext[si];
     }
     __syncthreads();
   }
@@ -474,7 +550,7 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
           const float v = acc[mt][si][r];
           if (direct) {
             _Float16 out = (_Float16)v;
-            if (bias != nullptr) out = (_Float16)((float)out + (float)as_h(bias[n]));
+            if (bias != nullptr) out = out + as_h(bias[n]);
             y[(size_t)m * ldy + n] = h_bits(out);
           } else {
             part[((size_t)split * M + m) * N + n] = v;
@@ -496,7 +572,7 @@ __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M,
   const int m = (int)(o / N);
   const int n = (int)(o % N);
   _Float16 out = (_Float16)sum;
-  if (bias != nullptr) out = (_Float16)((float)out + (float)as_h(bias[n]));
+  if (bias != nullptr) out = out + as_h(bias[n]);
   y[(size_t)m * ldy + n] = h_bits(out);
 }
 
@@ -524,13 +600,16 @@ __global__ void dequant_kernel(const u4* __restrict__ pq, const uint32_t* __rest
     const int g = k0 / gs;
     const uint32_t zw = pz[((size_t)s * G + g) * 2 + (j >> 3)];
     const int ze = (int)((zw >> ((j & 7) * 4)) & 15u) + 1;
-    const float sc = (float)as_h(ps[((size_t)s * G + g) * 16 + j]);
+    const _Float16 sc = as_h(ps[((size_t)s * G + g) * 16 + j]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int slot = (e & 1) ? 4 + (e >> 1) : (e >> 1);
       const int qv = (int)((q[t] >> (4 * slot)) & 15u);
-      // exact product of an fp16 and an integer |d| <= 16, rounded once
-      const _Float16 v = (_Float16)(sc * (float)(qv - ze));
+      // One IEEE fp16 multiply (round to nearest even) of the scale and the
+      // exact integer |q - z| <= 16.  Not written as an fp32 product
+      // narrowed to fp16: that form may be contracted into a mixed-precision
+      // FMA with a +0 addend, which turns a -0 product into +0.
+      const _Float16 v = sc * (_Float16)(qv - ze);
       const int k = k0 + e;
       const int row = perm ? perm[k] : k;
       w[(size_t)row * ldw + n] = h_bits(v);
@@ -552,36 +631,39 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
   return hipGetLastError();
 }
 
-hipError_t launch_gather_x(const uint16_t* x, int64_t ldx, const int32_t* perm, uint16_t* xg,
-                           int M, int K, hipStream_t stream) {
-  const size_t total = (size_t)M * K;
-  gather_x_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(x, ldx, perm, xg, M, K);
+template <int MT, bool G128, bool ACT>
+static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, float* part,
+                                    hipStream_t stream) {
+  const dim3 grid(a.N / kStripN, p.splits);
+  const dim3 block(kDecodeWaves * 64);
+  decode_kernel<MT, kDecodeWaves, kDecodePrefetch, G128, ACT><<<grid, block, p.smem, stream>>>(
+      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
+      a.bias, a.y, a.ldy, part, a.K, a.N, a.gs, a.G, p.cps);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || p.splits == 1) return err;
+  const size_t total = (size_t)a.M * a.N;
+  reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(part, p.splits, a.M, a.N,
+                                                                     a.bias, a.y, a.ldy);
   return hipGetLastError();
 }
 
 template <int MT>
-static hipError_t launch_decode_mt(const GemmArgs& a, hipStream_t stream) {
-  const dim3 grid(a.N / kStripN);
-  const dim3 block(kDecodeWaves * 64);
+static hipError_t launch_decode_mt(const GemmArgs& a, const DecodePlan& p, float* part,
+                                   hipStream_t stream) {
   const bool g128 = (a.gs % kChunkK) == 0;
-  if (g128)
-    decode_kernel<MT, kDecodeWaves, kDecodePrefetch, true><<<grid, block, 0, stream>>>(
-        (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, (const uint32_t*)a.pz, a.ps, a.bias,
-        a.y, a.ldy, a.K, a.gs, a.G);
-  else
-    decode_kernel<MT, kDecodeWaves, kDecodePrefetch, false><<<grid, block, 0, stream>>>(
-        (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, (const uint32_t*)a.pz, a.ps, a.bias,
-        a.y, a.ldy, a.K, a.gs, a.G);
-  return hipGetLastError();
+  const bool act = a.perm != nullptr;
+  if (g128) return act ? launch_decode_cfg<MT, true, true>(a, p, part, stream)
+                       : launch_decode_cfg<MT, true, false>(a, p, part, stream);
+  return act ? launch_decode_cfg<MT, false, true>(a, p, part, stream)
+             : launch_decode_cfg<MT, false, false>(a, p, part, stream);
 }
 
-hipError_t launch_decode(const GemmArgs& a, hipStream_t stream) {
-  const int mt = (a.M + 15) / 16;
-  switch (mt) {
-    case 1: return launch_decode_mt<1>(a, stream);
-    case 2: return launch_decode_mt<2>(a, stream);
-    case 3: return launch_decode_mt<3>(a, stream);
-    case 4: return launch_decode_mt<4>(a, stream);
+hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream) {
+  switch ((a.M + 15) / 16) {
+    case 1: return launch_decode_mt<1>(a, p, part, stream);
+    case 2: return launch_decode_mt<2>(a, p, part, stream);
+    case 3: return launch_decode_mt<3>(a, p, part, stream);
+    case 4: return launch_decode_mt<4>(a, p, part, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -597,7 +679,7 @@ static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, float* part,
   const int real_splits = (KC + cps - 1) / cps;
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
   prefill_kernel<MT2, S, ACT, G128><<<grid, 256, 0, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, (const uint32_t*)a.pz, a.ps,
+      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
       a.bias, a.y, a.ldy, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || real_splits == 1) return err;

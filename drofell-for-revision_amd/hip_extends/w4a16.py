@@ -32,10 +32,9 @@ from . import _lib
 class TuningParams:
     # Flattened M at or below which the register-dequant decode kernel runs
     # (at most 64: four 16-row MFMA tiles); above it the prefill kernel runs.
-    DECODE_MAX_M: int = 64
+    DECODE_MAX_M: int = 16
     # Largest flattened M the shared workspace is sized for.  Larger calls
-    # still run, without split-K (and raise for act-order decode, which
-    # cannot run without its gather buffer).
+    # still run, with the prefill kernel unsplit along K.
     MAX_M: int = 4096
     # Prefill split-K factor; 0 lets the library choose from the tile count.
     PREFILL_SPLIT_K: int = 0

@@ -51,7 +51,6 @@ def test_query_sizes_preserve_checkpoint_bytes():
         assert sizes["perm"] == 0
     act = _lib.query_sizes(5120, 13824, 128, True, 64)
     assert act["perm"] == 5120 * 4
-    assert act["workspace"] >= 64 * 5120 * 2  # act-order decode gather buffer
 
 
 def test_shape_validation_codes():
@@ -60,6 +59,8 @@ def test_shape_validation_codes():
     assert st == _lib.DW4_ERR_UNSUPPORTED
     st = lib.dw4_query_sizes(4096, 4096, 48, 0, 1, None, None, None, None, None)
     assert st == _lib.DW4_ERR_UNSUPPORTED
+    st = lib.dw4_query_sizes(4096, 4096, 96, 0, 1, None, None, None, None, None)
+    assert st == _lib.DW4_ERR_UNSUPPORTED  # a 128-row chunk would straddle groups
     st = lib.dw4_query_sizes(0, 4096, 128, 0, 1, None, None, None, None, None)
     assert st == _lib.DW4_ERR_INVALID_ARG
     # gemm / repack / dequant reject before touching a device
@@ -100,8 +101,14 @@ def test_make_perm_rejects_bad_g_idx():
 
 
 def test_workspace_size_rules():
+    # M=1 activations fit the decode workgroup's LDS: one split, no workspace
     assert _lib.workspace_size(1, 4096, 4096, 128, False) == 0
-    assert _lib.workspace_size(8, 4096, 4096, 128, True) == 8 * 4096 * 2
+    assert _lib.workspace_size(1, 13824, 5120, 128, True) == 0
+    # act-order gathers while staging: no gather buffer
+    assert _lib.workspace_size(8, 4096, 4096, 128, True) == _lib.workspace_size(8, 4096, 4096, 128, False)
+    # M=16 x K=11008 does not fit one workgroup's LDS: fp32 split-K planes
+    ws = _lib.workspace_size(16, 11008, 4096, 128, False)
+    assert ws > 0 and ws % (16 * 4096 * 4) == 0
     ws = _lib.workspace_size(256, 4096, 4096, 128, False)
     assert ws % (256 * 4096 * 4) == 0  # whole fp32 split-K partial planes
 

@@ -274,11 +274,13 @@ def test_errors_surface(hip_device):
     st = lib.dw4_gemm(1, 96, 4096, 32, x.data_ptr(), 96, q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
                       q4.scales.data_ptr(), None, None, y.data_ptr(), 4096, None, 0, None)
     assert st == _lib.DW4_ERR_UNSUPPORTED
-    say("errors: act-order decode without workspace")
-    perm = torch.arange(4096, dtype=torch.int32, device=hip_device)
-    st = lib.dw4_gemm(1, 4096, 4096, 128, x.data_ptr(), 4096, q4.qweight.data_ptr(),
-                      q4.qzeros.data_ptr(), q4.scales.data_ptr(), perm.data_ptr(), None,
-                      y.data_ptr(), 4096, None, 0, None)
+    say("errors: split decode without workspace")
+    # M=16 x K=4096 activations exceed one workgroup's LDS: fp32 split-K partials needed
+    xs = torch.zeros(16, 4096, dtype=torch.float16, device=hip_device)
+    ys = torch.empty(16, 4096, dtype=torch.float16, device=hip_device)
+    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 16, 4096, 4096, 128, xs.data_ptr(), 4096,
+                           q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(), None,
+                           None, ys.data_ptr(), 4096, None, 0, None)
     assert st == _lib.DW4_ERR_WORKSPACE
     say("errors: misaligned view goes through an aligned copy")
     xv = x[:, 1:4097]
