@@ -81,7 +81,7 @@ bool use_decode(int path, int m) {
 size_t workspace_for(int path, int m, int k, int n, int group_size) {
   if (m <= 0) return 0;
   if (use_decode(path, m)) {
-    const dw4::DecodePlan p = dw4::plan_decode(m, k, group_size);
+    const dw4::DecodePlan p = dw4::plan_decode(m, k, n, group_size, cu_count());
     return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
   }
   const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
@@ -211,7 +211,7 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
   a.ldy = ldy;
 
   if (decode) {
-    const dw4::DecodePlan plan = dw4::plan_decode(m, k, group_size);
+    const dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
     float* part = nullptr;
     if (plan.splits > 1) {
       const size_t need = (size_t)plan.splits * m * n * sizeof(float);

@@ -6,25 +6,23 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#ifndef DW4_DECODE_WAVES
-#define DW4_DECODE_WAVES 8
-#endif
-#ifndef DW4_DECODE_PREFETCH
-#define DW4_DECODE_PREFETCH 8
-#endif
 
 namespace dw4 {
 
 constexpr int kChunkK = 128;  // sorted rows per packed chunk
 constexpr int kStripN = 16;   // columns per strip
-constexpr int kDecodeWaves = DW4_DECODE_WAVES;
-constexpr int kDecodePrefetch = DW4_DECODE_PREFETCH;
 constexpr int kDecodeMaxM = 64;      // four 16-row MFMA tiles
 constexpr int kDecodeAutoMaxM = 16;  // DW4_PATH_AUTO picks decode up to this M
-// LDS a decode workgroup may use for its staged activations and metadata;
-// a K range whose slice does not fit is split across workgroups.
-constexpr size_t kDecodeLdsBudget = 64 * 1024;
 constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
+#ifndef DW4_DECODE_UMAX
+#define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
+#endif
+#ifndef DW4_DECODE_NARROW_WAVES
+#define DW4_DECODE_NARROW_WAVES 16  // waves per workgroup when strips <= CUs and M <= 4
+#endif
+constexpr int kDecodeUMax = DW4_DECODE_UMAX;
+constexpr int kDecodeNarrowWaves = DW4_DECODE_NARROW_WAVES;
+constexpr size_t kLdsPerCu = 160 * 1024;
 
 struct GemmArgs {
   int M, K, N, gs, G;
@@ -46,28 +44,42 @@ struct PrefillPlan {
 struct DecodePlan {
   int splits;   // workgroups along K per strip
   int cps;      // 128-row chunks per split
+  int waves;    // waves per workgroup (4 or 8)
   size_t smem;  // dynamic LDS bytes per workgroup
 };
 
-// LDS bytes a decode workgroup needs for a K range of `cps` chunks.
-inline size_t decode_smem_bytes(int m, int cps, int gs) {
-  const size_t rows = (size_t)cps * kChunkK;
-  const size_t groups = rows / (size_t)gs + 2;
-  const size_t staged = (size_t)m * (rows + 8) * 2 + groups * kMetaBytes;
+// LDS bytes a decode workgroup needs for a K range of `cps` chunks: each of
+// its waves stages the activation rows and metadata records of its own
+// ceil(cps / waves) chunks; the reduction reuses the space afterwards.
+inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
+  const size_t per_wave = (size_t)((cps + waves - 1) / waves);
+  const size_t rec = (size_t)(gs < kChunkK ? kChunkK / gs : 1) * kMetaBytes;
+  const size_t staged = (size_t)waves * per_wave * ((size_t)m * (kChunkK + 8) * 2 + rec);
   const size_t mt = (size_t)((m + 15) / 16);
-  const size_t red = (size_t)kDecodeWaves * mt * 64 * 16;
+  const size_t red = (size_t)waves * mt * 64 * 16;
   const size_t b = staged > red ? staged : red;
   return (b + 15) & ~(size_t)15;
 }
 
-// Fewest K splits whose per-workgroup slice fits the LDS budget.
-inline DecodePlan plan_decode(int m, int k, int gs) {
+// Waves per workgroup: enough to fill the chip with the strips available
+// (one workgroup per 16-column strip), fewer for larger M whose activation
+// slices are bigger.  K is split across workgroups only where the staged
+// activations would not fit the LDS share of one workgroup (the CU's LDS
+// divided by the workgroups it is expected to hold).
+inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus) {
   const int kc = k / kChunkK;
-  DecodePlan p{1, kc, decode_smem_bytes(m, kc, gs)};
+  const int strips = n / kStripN;
+  int waves = 8;
+  if (strips >= 2 * cus && m <= 16) waves = 4;
+  else if (strips <= cus && m <= 4) waves = kDecodeNarrowWaves;
+  const int wgs_per_cu = (strips + cus - 1) / cus;
+  size_t budget = kLdsPerCu / (size_t)(wgs_per_cu > 0 ? wgs_per_cu : 1) - 1024;
+  if (budget > 144 * 1024) budget = 144 * 1024;
+  DecodePlan p{1, kc, waves, decode_smem_bytes(m, kc, gs, waves)};
   for (int s = 1; s <= kc; ++s) {
     const int cps = (kc + s - 1) / s;
-    const size_t bytes = decode_smem_bytes(m, cps, gs);
-    if (bytes <= kDecodeLdsBudget || s == kc) {
+    const size_t bytes = decode_smem_bytes(m, cps, gs, waves);
+    if (bytes <= budget || s == kc) {
       p.splits = (kc + cps - 1) / cps;
       p.cps = cps;
       p.smem = bytes;

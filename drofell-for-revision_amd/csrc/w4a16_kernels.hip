@@ -35,27 +35,39 @@ __device__ __forceinline__ _Float16 as_h(uint16_t u) { return __builtin_bit_cast
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ h2 splat2(_Float16 v) { return h2{v, v}; }
 
+// (a & mask) | magic in one VALU instruction.  Written out because the
+// compiler splits it into two when both constants are literals (a gfx9 VOP3
+// instruction cannot encode two literals); here the mask comes from an SGPR
+// and the magic value from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
+  return r;
+}
+
 // The 8 rows of one packed word, minus the effective zero, as exact fp16
 // integers in row order.  Even rows sit in the low half-word, odd rows in
 // the high half-word, so OR-ing a nibble pair into the fp16 pattern of
 // 1024.0 yields (1024 + q) or (1024 + 16 q) in each half without a shift.
-__device__ __forceinline__ h8 centered8(uint32_t w, h2 nz1024, h2 nz64) {
+__device__ __forceinline__ h8 centered8(uint32_t w, h2 nz1024, h2 nz64, uint32_t magic) {
   const h2 sixteenth = splat2((_Float16)0.0625f);
   const uint32_t w8 = w >> 8;
-  const h2 p0 = as_h2((w & 0x000F000Fu) | kMagic) + nz1024;               // rows 0,1
-  const h2 p1 = as_h2((w & 0x00F000F0u) | kMagic) * sixteenth + nz64;     // rows 2,3
-  const h2 p2 = as_h2((w8 & 0x000F000Fu) | kMagic) + nz1024;              // rows 4,5
-  const h2 p3 = as_h2((w8 & 0x00F000F0u) | kMagic) * sixteenth + nz64;    // rows 6,7
+  const h2 p0 = as_h2(and_or(w, 0x000F000Fu, magic)) + nz1024;               // rows 0,1
+  const h2 p1 = as_h2(and_or(w, 0x00F000F0u, magic)) * sixteenth + nz64;     // rows 2,3
+  const h2 p2 = as_h2(and_or(w8, 0x000F000Fu, magic)) + nz1024;              // rows 4,5
+  const h2 p3 = as_h2(and_or(w8, 0x00F000F0u, magic)) * sixteenth + nz64;    // rows 6,7
   const h4 a = __builtin_shufflevector(p0, p1, 0, 1, 2, 3);
   const h4 b = __builtin_shufflevector(p2, p3, 0, 1, 2, 3);
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Zero-point constants -(1024 + z_eff) and -(64 + z_eff) from a stored nibble.
+// Zero-point constants -(1024 + z_eff) and -(64 + z_eff) (z_eff = stored + 1,
+// 1..16) built from their fp16 bit patterns: 1024 + z has exponent 10 and
+// mantissa z, 64 + z has exponent 6 and mantissa 16 z.
 __device__ __forceinline__ void zero_consts(uint32_t zword, int zshift, h2& nz1024, h2& nz64) {
-  const int ze = (int)((zword >> zshift) & 15u) + 1;
-  nz1024 = splat2((_Float16)(float)(-(1024 + ze)));
-  nz64 = splat2((_Float16)(float)(-(64 + ze)));
+  const uint32_t ze = ((zword >> zshift) & 15u) + 1u;
+  nz1024 = as_h2((0xE400u | ze) * 0x00010001u);
+  nz64 = as_h2((0xD400u | (ze << 4)) * 0x00010001u);
 }
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
@@ -146,19 +158,21 @@ __device__ __forceinline__ h8 load_x_unit(const _Float16* __restrict__ row,
 }
 
 // ---------------------------------------------------------------------------
-// Decode kernel (M <= 64).  Grid: (N/16 strips) x (K splits).  The
-// workgroup first stages its activation slice (gathered for act-order) and
-// the strip's scales/zeros for its K range in LDS, while the packed weight
-// words stream into a U-deep register ring (non-temporal 16-byte loads,
-// 1 KB contiguous per wave).  Its waves take interleaved 128-row chunks;
-// each word is dequantised in registers straight into the B operand of
-// v_mfma_f32_16x16x32_f16 (exact q - z in fp16), the scale is applied per
-// group in fp32, and the waves' partial sums meet in LDS in a fixed order.
-// The only global loads inside the main loop are the weight ring's, so no
-// wait in the loop covers more than the oldest ring slot.
+// Decode kernel (M <= 64).  Grid: (N/16 strips) x (K splits).  Each wave
+// owns the interleaved 128-row chunks lc = wave + i*WAVES of its workgroup's
+// K range.  It stages the activation slices (gathered for act-order) and the
+// scale/zero records of exactly those chunks into a private LDS region and
+// reads back only its own region, so no workgroup barrier stands between a
+// wave's first weight bytes and its first MFMA.  The packed weight words
+// stream into a U-deep register ring (non-temporal 16-byte loads, 1 KB
+// contiguous per wave instruction); each word is dequantised in registers
+// straight into the B operand of v_mfma_f32_16x16x32_f16 (exact q - z in
+// fp16); the scale is applied per group in fp32; the waves' partial sums
+// meet in LDS in a fixed order at the end (deterministic).
 // ---------------------------------------------------------------------------
-constexpr int kXBatch = 4;  // activation units per thread per staging pass
-constexpr int kMBatch = 4;  // metadata dwords per thread per staging pass
+constexpr int kXBatch = 4;  // activation units per lane in the first staging pass
+constexpr int kMBatch = 4;  // metadata dwords per lane in the first staging pass
+constexpr int kLdx = kChunkK + 8;  // halfs per staged activation row (16-byte pad)
 
 template <int MT, int WAVES, int U, bool G128, bool ACT>
 __global__ void __launch_bounds__(WAVES * 64)
@@ -173,104 +187,106 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
   const int split = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar math
   const int j = lane & 15;
   const int kq = lane >> 4;
   const int KC = K / kChunkK;
   const int c0 = split * cps;
   const int nc = min(KC, c0 + cps) - c0;
-  const int kr = nc * kChunkK;
-  const int ldl = kr + 8;  // halfs per staged row: 16-byte pad against bank conflicts
-  const int g0 = (c0 * kChunkK) / gs;
-  const int ng = ((c0 + nc) * kChunkK - 1) / gs - g0 + 1;
-  _Float16* xs = reinterpret_cast<_Float16*>(smem);
-  uint32_t* ms = reinterpret_cast<uint32_t*>(smem + (size_t)M * ldl * 2);
+  const int nch = wave < nc ? (nc - wave + WAVES - 1) / WAVES : 0;  // this wave's chunks
+  const int nch_max = (cps + WAVES - 1) / WAVES;                      // region size
+  const int gpc = G128 ? 1 : kChunkK / gs;  // metadata records per chunk
+  const int rec = gpc * kMetaWords;         // metadata dwords per chunk
 
-  const int xrow_units = kr >> 3;
-  const int xunits = M * xrow_units;
-  const int munits = ng * kMetaWords;
-  const int kbase = c0 * kChunkK;
+  // this wave's private LDS: activations [chunk][row][kLdx] then metadata
+  _Float16* xw = reinterpret_cast<_Float16*>(smem) + (size_t)wave * nch_max * M * kLdx;
+  uint32_t* mw = reinterpret_cast<uint32_t*>(reinterpret_cast<_Float16*>(smem) +
+                                             (size_t)WAVES * nch_max * M * kLdx) +
+                 (size_t)wave * nch_max * rec;
 
-  // staging pass 0: issued before the weight ring so the wait for it does
-  // not cover the ring's loads
+  const int xupc = M * 16;  // 16-byte activation units per chunk
+  const int xunits = nch * xupc;
+  const int munits = nch * rec;
+  auto x_unit = [&](int u) -> h8 {
+    const int i = u / xupc;
+    const int r = u - i * xupc;
+    const int m = r >> 4;
+    const int k = (c0 + wave + i * WAVES) * kChunkK + (r & 15) * 8;
+    return load_x_unit<ACT>(x + (size_t)m * ldx, perm, k);
+  };
+  auto x_dst = [&](int u) -> _Float16* {
+    const int i = u / xupc;
+    const int r = u - i * xupc;
+    return xw + ((size_t)i * M + (r >> 4)) * kLdx + (r & 15) * 8;
+  };
+  auto m_word = [&](int v) -> uint32_t {
+    const int i = v / rec;
+    const int r = v - i * rec;
+    const int gl = r / kMetaWords;
+    const int c = c0 + wave + i * WAVES;
+    const int g = G128 ? (c * kChunkK) / gs : c * gpc + gl;
+    return meta_word(ps32, pz, G, s, g, r - gl * kMetaWords);
+  };
+
+  // staging pass 0, issued before the weight ring so that waiting for it
+  // does not wait for the ring
   h8 xv[kXBatch];
   uint32_t mv[kMBatch];
 #pragma unroll
-  for (int b = 0; b < kXBatch; ++b) {
-    const int u = tid + b * T;
-    if (u < xunits) {
-      const int m = u / xrow_units;
-      xv[b] = load_x_unit<ACT>(x + (size_t)m * ldx, perm, kbase + (u - m * xrow_units) * 8);
-    }
-  }
+  for (int b = 0; b < kXBatch; ++b)
+    if (lane + 64 * b < xunits) xv[b] = x_unit(lane + 64 * b);
 #pragma unroll
-  for (int b = 0; b < kMBatch; ++b) {
-    const int v = tid + b * T;
-    if (v < munits) mv[b] = meta_word(ps32, pz, G, s, g0 + v / kMetaWords, v % kMetaWords);
-  }
+  for (int b = 0; b < kMBatch; ++b)
+    if (lane + 64 * b < munits) mv[b] = m_word(lane + 64 * b);
 
-  // weight ring
+  // weight ring.  With U >= 2 the host guarantees every wave at least U
+  // chunks, so the prologue loads are unconditional.
   const u4* qp = pq + ((size_t)s * KC + c0) * 64 + lane;
-  const int nch = wave < nc ? (nc - wave + WAVES - 1) / WAVES : 0;
   u4 qb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (u < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + u * WAVES) * 64);
+    if (U >= 2 || u < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + u * WAVES) * 64);
 
 #pragma unroll
-  for (int b = 0; b < kXBatch; ++b) {
-    const int u = tid + b * T;
-    if (u < xunits) {
-      const int m = u / xrow_units;
-      *(h8*)(xs + (size_t)m * ldl + (u - m * xrow_units) * 8) = xv[b];
-    }
-  }
+  for (int b = 0; b < kXBatch; ++b)
+    if (lane + 64 * b < xunits) *(h8*)x_dst(lane + 64 * b) = xv[b];
 #pragma unroll
-  for (int b = 0; b < kMBatch; ++b) {
-    const int v = tid + b * T;
-    if (v < munits) ms[v] = mv[b];
-  }
-  // further passes (large M*K or many groups)
-  for (int u = tid + kXBatch * T; u < xunits; u += T) {
-    const int m = u / xrow_units;
-    const int c8 = u - m * xrow_units;
-    *(h8*)(xs + (size_t)m * ldl + c8 * 8) =
-        load_x_unit<ACT>(x + (size_t)m * ldx, perm, kbase + c8 * 8);
-  }
-  for (int v = tid + kMBatch * T; v < munits; v += T)
-    ms[v] = meta_word(ps32, pz, G, s, g0 + v / kMetaWords, v % kMetaWords);
-  __syncthreads();
+  for (int b = 0; b < kMBatch; ++b)
+    if (lane + 64 * b < munits) mw[lane + 64 * b] = mv[b];
+  for (int u = lane + 64 * kXBatch; u < xunits; u += 64) *(h8*)x_dst(u) = x_unit(u);
+  for (int v = lane + 64 * kMBatch; v < munits; v += 64) mw[v] = m_word(v);
+  // The wave reads back only what it wrote; LDS operations of one wave
+  // complete in order, so no workgroup barrier is needed here.
 
   const int zsh = (j & 7) * 4;
-  const _Float16* xl[MT];
-  bool xok[MT];
+  const uint32_t magic = kMagic;
+  // A-operand rows: lanes past the last row read row M-1.  Output row i of
+  // an MFMA depends only on A row i, and rows >= M are never stored.
+  int xrow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + j;
-    xok[mt] = m < M;
-    xl[mt] = xs + (size_t)(xok[mt] ? m : 0) * ldl + kq * 8;
-  }
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + j, M - 1) * kLdx + kq * 8;
   f4 tot[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) tot[mt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  // One chunk: 4 k-steps of 32 rows; w holds this lane's 4 packed words.
-  auto chunk = [&](const u4 w, int lc) {
-    const int kl = lc * kChunkK;
+  // One chunk (the wave's i-th): 4 k-steps of 32 rows; w holds this lane's
+  // 4 packed words.
+  auto chunk = [&](const u4 w, int i) {
+    const _Float16* xc = xw + (size_t)i * M * kLdx;
+    const uint32_t* mr = mw + i * rec;
     f4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
     if (G128) {
-      const uint32_t* mr = ms + (((c0 + lc) * kChunkK) / gs - g0) * kMetaWords;
       const float sc = (float)reinterpret_cast<const _Float16*>(mr)[j];
       h2 nz1024, nz64;
       zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const h8 b = centered8(w[t], nz1024, nz64);
+        const h8 b = centered8(w[t], nz1024, nz64, magic);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const h8 a = xok[mt] ? *(const h8*)(xl[mt] + kl + 32 * t) : h8{};
+          const h8 a = *(const h8*)(xc + xrow[mt] + 32 * t);
           acc[mt] = mfma16(a, b, acc[mt]);
         }
       }
@@ -284,14 +300,14 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         if (t % spg == 0) {
-          const uint32_t* mr = ms + (((c0 + lc) * kChunkK + 32 * t) / gs - g0) * kMetaWords;
-          sc = (float)reinterpret_cast<const _Float16*>(mr)[j];
-          zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
+          const uint32_t* mg = mr + (t / spg) * kMetaWords;
+          sc = (float)reinterpret_cast<const _Float16*>(mg)[j];
+          zero_consts(mg[8 + (j >> 3)], zsh, nz1024, nz64);
         }
-        const h8 b = centered8(w[t], nz1024, nz64);
+        const h8 b = centered8(w[t], nz1024, nz64, magic);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const h8 a = xok[mt] ? *(const h8*)(xl[mt] + kl + 32 * t) : h8{};
+          const h8 a = *(const h8*)(xc + xrow[mt] + 32 * t);
           acc[mt] = mfma16(a, b, acc[mt]);
         }
         if (t % spg == spg - 1) {
@@ -311,9 +327,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
   for (; i0 + 2 * U <= nch; i0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int lc = wave + (i0 + u) * WAVES;
-      chunk(qb[u], lc);  // consume, then refill the same registers
-      qb[u] = __builtin_nontemporal_load(qp + (size_t)(lc + U * WAVES) * 64);
+      chunk(qb[u], i0 + u);  // consume, then refill the same registers
+      qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + (i0 + u + U) * WAVES) * 64);
     }
   }
   // Drain: at most 2U - 1 chunks left; refills only where a chunk remains.
@@ -321,15 +336,14 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
   for (int u = 0; u < U; ++u) {
     const int i = i0 + u;
     if (i < nch) {
-      const int lc = wave + i * WAVES;
-      chunk(qb[u], lc);
-      if (i + U < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(lc + U * WAVES) * 64);
+      chunk(qb[u], i);
+      if (i + U < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + (i + U) * WAVES) * 64);
     }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int i = i0 + U + u;
-    if (i < nch) chunk(qb[u], wave + i * WAVES);
+    if (i < nch) chunk(qb[u], i);
   }
 
   __syncthreads();  // staged activations are dead; reuse LDS for the reduction
@@ -497,6 +511,7 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   __syncthreads();
 
   const int zsh = (j & 7) * 4;
+  const uint32_t magic = kMagic;
   for (int c = c_begin; c < c_end; ++c) {
     const int buf = (c - c_begin) & 1;
     const bool has_next = (c + 1) < c_end;
@@ -517,7 +532,7 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
         const _Float16 sc = reinterpret_cast<const _Float16*>(mr)[j];
         h2 nz1024, nz64;
         zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
-        const h8 d = centered8(qcur[si][t], nz1024, nz64);
+        const h8 d = centered8(qcur[si][t], nz1024, nz64, magic);
         const h8 s8 = h8{sc, sc, sc, sc, sc, sc, sc, sc};
         bop[si] = d * s8;  // fp16 product, round to nearest even
       }
@@ -631,12 +646,21 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
   return hipGetLastError();
 }
 
-template <int MT, bool G128, bool ACT>
+template <int MT, int WAVES, int U, bool G128, bool ACT>
 static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, float* part,
                                     hipStream_t stream) {
   const dim3 grid(a.N / kStripN, p.splits);
-  const dim3 block(kDecodeWaves * 64);
-  decode_kernel<MT, kDecodeWaves, kDecodePrefetch, G128, ACT><<<grid, block, p.smem, stream>>>(
+  if (p.smem > 64 * 1024) {
+    static bool raised = false;  // idempotent attribute; races only repeat it
+    if (!raised) {
+      const hipError_t e = hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&decode_kernel<MT, WAVES, U, G128, ACT>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsPerCu);
+      if (e != hipSuccess) return e;
+      raised = true;
+    }
+  }
+  decode_kernel<MT, WAVES, U, G128, ACT><<<grid, WAVES * 64, p.smem, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
       a.bias, a.y, a.ldy, part, a.K, a.N, a.gs, a.G, p.cps);
   hipError_t err = hipGetLastError();
@@ -647,15 +671,45 @@ static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, floa
   return hipGetLastError();
 }
 
+template <int MT, int WAVES, bool G128>
+static hipError_t launch_decode_g(const GemmArgs& a, const DecodePlan& p, float* part,
+                                  hipStream_t stream) {
+  // Ring depth: the largest of 8, 4, 2 that every wave can fill (the shortest
+  // wave gets floor(chunks / waves) chunks); 1 (conditional prologue)
+  // otherwise.  Group sizes 32/64 keep more per-chunk state live, so their
+  // rings are shallower to stay within registers.
+  // (measured: deeper rings only lengthen the initial request burst that
+  // every wave's activation loads queue behind)
+  constexpr int UMAX = G128 ? (WAVES >= 16 ? 2 : kDecodeUMax) : (WAVES >= 16 ? 2 : 4);
+  const int KC = a.K / kChunkK;
+  const int last = min(p.cps, KC - (p.splits - 1) * p.cps);  // shortest split
+  const int per_wave = last / WAVES;
+  const bool act = a.perm != nullptr;
+#define DW4_DECODE_U(UU)                                                                  \
+  return act ? launch_decode_cfg<MT, WAVES, UU, G128, true>(a, p, part, stream)            \
+             : launch_decode_cfg<MT, WAVES, UU, G128, false>(a, p, part, stream)
+  if (UMAX >= 8 && per_wave >= 8) { DW4_DECODE_U(UMAX >= 8 ? 8 : 1); }
+  if (UMAX >= 4 && per_wave >= 4) { DW4_DECODE_U(UMAX >= 4 ? 4 : 1); }
+  if (per_wave >= 2) { DW4_DECODE_U(2); }
+  DW4_DECODE_U(1);
+#undef DW4_DECODE_U
+}
+
+template <int MT, int WAVES>
+static hipError_t launch_decode_w(const GemmArgs& a, const DecodePlan& p, float* part,
+                                  hipStream_t stream) {
+  if ((a.gs % kChunkK) == 0) return launch_decode_g<MT, WAVES, true>(a, p, part, stream);
+  return launch_decode_g<MT, WAVES, false>(a, p, part, stream);
+}
+
 template <int MT>
 static hipError_t launch_decode_mt(const GemmArgs& a, const DecodePlan& p, float* part,
                                    hipStream_t stream) {
-  const bool g128 = (a.gs % kChunkK) == 0;
-  const bool act = a.perm != nullptr;
-  if (g128) return act ? launch_decode_cfg<MT, true, true>(a, p, part, stream)
-                       : launch_decode_cfg<MT, true, false>(a, p, part, stream);
-  return act ? launch_decode_cfg<MT, false, true>(a, p, part, stream)
-             : launch_decode_cfg<MT, false, false>(a, p, part, stream);
+  if constexpr (MT == 1) {  // 4- and 16-wave workgroups are planned for M <= 16 only
+    if (p.waves == 4) return launch_decode_w<MT, 4>(a, p, part, stream);
+    if (p.waves == 16) return launch_decode_w<MT, 16>(a, p, part, stream);
+  }
+  return launch_decode_w<MT, 8>(a, p, part, stream);
 }
 
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream) {
