@@ -45,18 +45,21 @@ int check_shape(int k, int n, int group_size) {
 
 int status_of(hipError_t e) { return e == hipSuccess ? DW4_OK : DW4_ERR_LAUNCH; }
 
+size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n);
+
 // Prefill tiling and split-K factor for one call.  `ws_bytes` caps the
 // split count: with too little workspace the call runs unsplit.
 dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_bytes, bool cap_by_ws) {
   dw4::PrefillPlan p;
-  p.bm = m <= 64 ? 64 : 128;
-  p.bn = 128;
+  p.bm = m <= 512 ? 64 : 128;
+  p.bn = n >= 2048 ? 256 : 128;
+  p.occ = (p.bm == 64 && p.bn == 256) ? DW4_PREFILL_OCC : 1;
   const int kc = k / kChunkK;
   const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
   int splits = split_req;
   if (splits <= 0) {
-    const int cus = cu_count();
-    splits = tiles >= cus ? 1 : cus / tiles;
+    const int slots = cu_count() * p.occ;  // workgroups resident at once
+    splits = tiles >= slots ? 1 : slots / tiles;
     splits = std::min(splits, std::max(1, kc / 4));
     splits = std::min(splits, 16);
   }
@@ -64,12 +67,15 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
   // the launcher rounds to whole chunks per split
   const int cps = (kc + splits - 1) / splits;
   splits = (kc + cps - 1) / cps;
-  if (cap_by_ws && splits > 1) {
-    const size_t per_split = (size_t)m * n * sizeof(float);
-    if ((size_t)splits * per_split > ws_bytes) splits = 1;
-  }
+  if (tiles > dw4::kSplitCounters) splits = 1;  // one arrival counter per tile
   p.splits = splits;
+  if (cap_by_ws && splits > 1 && prefill_ws_bytes(p, m, n) > ws_bytes) p.splits = 1;
   return p;
+}
+
+size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n) {
+  const size_t mt = (size_t)(m + p.bm - 1) / p.bm, nt = (size_t)(n + p.bn - 1) / p.bn;
+  return dw4::split_ws_bytes(p.splits, mt * nt * p.bm * p.bn);
 }
 
 bool use_decode(int path, int m) {
@@ -82,10 +88,10 @@ size_t workspace_for(int path, int m, int k, int n, int group_size) {
   if (m <= 0) return 0;
   if (use_decode(path, m)) {
     const dw4::DecodePlan p = dw4::plan_decode(m, k, n, group_size, cu_count());
-    return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+    return dw4::split_ws_bytes(p.splits, (size_t)m * n);
   }
   const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
-  return p.splits > 1 ? (size_t)p.splits * m * n * sizeof(float) : 0;
+  return prefill_ws_bytes(p, m, n);
 }
 
 }  // namespace
@@ -214,24 +220,17 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
     const dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
     float* part = nullptr;
     if (plan.splits > 1) {
-      const size_t need = (size_t)plan.splits * m * n * sizeof(float);
+      const size_t need = dw4::split_ws_bytes(plan.splits, (size_t)m * n);
       if (workspace == nullptr || workspace_bytes < need) return DW4_ERR_WORKSPACE;
       if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
-      part = static_cast<float*>(workspace);
+      part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + dw4::kWsHeadBytes);
     }
     return status_of(dw4::launch_decode(a, plan, part, s));
   }
 
   dw4::PrefillPlan plan = plan_prefill(m, k, n, split_k, workspace ? workspace_bytes : 0, true);
-  float* part = nullptr;
-  if (plan.splits > 1) {
-    if (workspace == nullptr || !aligned16(workspace)) {
-      plan.splits = 1;
-    } else {
-      part = static_cast<float*>(workspace);
-    }
-  }
-  return status_of(dw4::launch_prefill(a, plan, part, s));
+  if (plan.splits > 1 && !aligned16(workspace)) plan.splits = 1;
+  return status_of(dw4::launch_prefill(a, plan, workspace, s));
 }
 
 int dw4_gemm(int m, int k, int n, int group_size, const uint16_t* x, int64_t ldx,

@@ -17,6 +17,12 @@ constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 #ifndef DW4_DECODE_UMAX
 #define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
 #endif
+#ifndef DW4_PREFILL_PB
+#define DW4_PREFILL_PB 4  // prefill weight ring depth (chunks) of the 64x256 tile
+#endif
+#ifndef DW4_PREFILL_OCC
+#define DW4_PREFILL_OCC 1  // workgroups per CU of the 64x256 prefill tile
+#endif
 #ifndef DW4_DECODE_NARROW_WAVES
 #define DW4_DECODE_NARROW_WAVES 16  // waves per workgroup when strips <= CUs and M <= 4
 #endif
@@ -39,6 +45,7 @@ struct GemmArgs {
 
 struct PrefillPlan {
   int bm, bn, splits;
+  int occ = 1;  // workgroups per CU the kernel variant is built for (1 or 2)
 };
 
 struct DecodePlan {
@@ -93,7 +100,19 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
                          const int32_t* perm, uint32_t* pq, uint32_t* pz, uint16_t* ps,
                          int K, int N, int G, hipStream_t stream);
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream);
-hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, float* part,
+// Workspace of a split-K call: a fixed head of kSplitCounters int32 arrival
+// counters (one per prefill output tile; zero before the first call and left
+// zero by every call), then one fp32 partial plane per split: [M][N] for the
+// decode kernel, [mtiles*ntiles][BM*BN] (whole tiles) for the prefill kernel.
+// The head has the same size and place for every call, so partials written by
+// one call never land on the counters of another.
+constexpr int kSplitCounters = 4096;
+constexpr size_t kWsHeadBytes = kSplitCounters * sizeof(int);
+inline size_t split_ws_bytes(int splits, size_t plane_floats) {
+  return splits > 1 ? kWsHeadBytes + (size_t)splits * plane_floats * sizeof(float) : 0;
+}
+
+hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* ws,
                           hipStream_t stream);
 hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,
                           const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,

@@ -378,33 +378,32 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 
 // ---------------------------------------------------------------------------
 // Prefill kernel (any M): 4 waves; workgroup tile (16*MT2) rows x (64*S)
-// columns.  Per 128-row chunk the workgroup stages the activation tile
-// (gathered for act-order) and the tile's scales/zeros into double-buffered
-// LDS; each wave owns S strips, streams their packed words into registers
-// one chunk ahead and dequantises them to the exact fp16 weight
-// (fp16_rne(scale * (q - z)), as the reference's dequantiser), which feeds
-// v_mfma_f32_16x16x32_f16 directly.  Split-K partials (fp32) go to the
-// workspace and are summed in a fixed order by reduce_kernel.
+// columns; waves split the columns (S strips each) and share the rows.
+// Activations (L2-resident) are staged per 128-row chunk into double-
+// buffered LDS one chunk ahead (gathered through perm for act-order).  Each
+// wave streams its strips' packed words and their scale/zero words through a
+// PB-deep register ring (the weights come from HBM, so the ring covers its
+// latency), dequantises them to the exact fp16 weight
+// fp16_rne(scale * (q - z)) -- the value the reference's dequantiser
+// produces -- and feeds v_mfma_f32_16x16x32_f16 directly.  With split-K
+// each split publishes an fp32 partial tile to the workspace and the last
+// split of a tile to arrive sums them in split order (deterministic).
 // ---------------------------------------------------------------------------
 constexpr int kLdaPad = 8;
 constexpr int kLda = kChunkK + kLdaPad;  // halfs per LDS row (272 bytes)
 
-template <int MT2, int S, bool ACT, bool G128>
-__global__ void __launch_bounds__(256)
+template <int MT2, int S, int PB, int GPC, bool ACT, int OCC>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                const int32_t* __restrict__ perm,
                const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
                const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
                uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
-               int K, int N, int gs, int G, int chunks_per_split, int mtiles, int ntiles) {
+               int* __restrict__ counters, int K, int N, int gs, int G, int chunks_per_split,
+               int mtiles, int ntiles) {
   constexpr int BM = 16 * MT2;
   constexpr int UNITS = BM * 16 / 256;  // 16-byte activation units per thread per chunk
-  constexpr int NSTRIP = 4 * S;
-  constexpr int GPC = G128 ? 1 : 4;     // group records per strip per chunk (max)
-  constexpr int MW = NSTRIP * GPC * kMetaWords;
-  constexpr int MU = (MW + 255) / 256;  // metadata dwords per thread per chunk
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLda];
-  __shared__ __attribute__((aligned(16))) uint32_t Ms[2][MW];
 
   // XCD-aware tile order: the M-tiles of one N-tile get block ids congruent
   // modulo 8, so they run on one XCD and share its L2 copy of the weights.
@@ -417,78 +416,69 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15;
   const int kq = lane >> 4;
   const int KC = K / kChunkK;
   const int split = blockIdx.y;
   const int c_begin = split * chunks_per_split;
-  const int c_end = min(KC, c_begin + chunks_per_split);
+  const int nchunks = min(KC, c_begin + chunks_per_split) - c_begin;
   const int m0 = mtile * BM;
   const int NS = N / kStripN;
-  const int gpc = G128 ? 1 : kChunkK / gs;  // 4 (gs 32) or 2 (gs 64)
-  const int strip_base = ntile * NSTRIP;
 
-  // activation staging: unit u -> (row, 16-byte column)
-  int arow[UNITS], acol[UNITS];
-  bool aval[UNITS];
+  // activation staging: unit u -> (row, 16-byte column); rows past M read
+  // row M-1 (their MFMA output rows are never stored)
+  const _Float16* arow[UNITS];
+  int aoff[UNITS];
 #pragma unroll
   for (int i = 0; i < UNITS; ++i) {
     const int u = tid + 256 * i;
-    arow[i] = u >> 4;
-    acol[i] = u & 15;
-    aval[i] = (m0 + arow[i]) < M;
+    arow[i] = x + (size_t)min(m0 + (u >> 4), M - 1) * ldx;
+    aoff[i] = (u >> 4) * kLda + (u & 15) * 8;
   }
   auto load_a = [&](int c, h8 (&regs)[UNITS]) {
 #pragma unroll
     for (int i = 0; i < UNITS; ++i)
-      regs[i] = aval[i] ? load_x_unit<ACT>(x + (size_t)(m0 + arow[i]) * ldx, perm,
-                                           c * kChunkK + acol[i] * 8)
-                        : h8{};
+      regs[i] = load_x_unit<ACT>(arow[i], perm, c * kChunkK + ((tid + 256 * i) & 15) * 8);
   };
   auto store_a = [&](int buf, const h8 (&regs)[UNITS]) {
 #pragma unroll
-    for (int i = 0; i < UNITS; ++i) *(h8*)(&As[buf][arow[i] * kLda + acol[i] * 8]) = regs[i];
-  };
-  // metadata staging: dword v -> (local strip, group within chunk, word)
-  const int mwords = NSTRIP * gpc * kMetaWords;
-  auto load_m = [&](int c, uint32_t (&regs)[MU]) {
-#pragma unroll
-    for (int i = 0; i < MU; ++i) {
-      const int v = tid + 256 * i;
-      regs[i] = 0u;
-      if (v < mwords) {
-        const int sl = v / (gpc * kMetaWords);
-        const int rem = v - sl * gpc * kMetaWords;
-        const int gl = rem / kMetaWords;
-        const int st = strip_base + sl;
-        if (st < NS)
-          regs[i] = meta_word(ps32, pz, G, st, (c * kChunkK) / gs + gl, rem - gl * kMetaWords);
-      }
-    }
-  };
-  auto store_m = [&](int buf, const uint32_t (&regs)[MU]) {
-#pragma unroll
-    for (int i = 0; i < MU; ++i) {
-      const int v = tid + 256 * i;
-      if (v < mwords) Ms[buf][v] = regs[i];
-    }
+    for (int i = 0; i < UNITS; ++i) *(h8*)(&As[buf][aoff[i]]) = regs[i];
   };
 
   // weight strips owned by this wave (the last N-tile may be partial)
-  const int strip0 = strip_base + wave * S;
+  const int strip0 = ntile * 4 * S + wave * S;
   const u4* qp[S];
+  const uint32_t* sp[S];  // dword holding this lane's fp16 scale (pair j & ~1, j | 1)
+  const uint32_t* zp[S];
   bool sval[S];
 #pragma unroll
   for (int si = 0; si < S; ++si) {
     const int st = strip0 + si;
     sval[si] = st < NS;
-    qp[si] = pq + (size_t)(sval[si] ? st : 0) * KC * 64 + lane;
+    const int sc = sval[si] ? st : 0;
+    qp[si] = pq + ((size_t)sc * KC + c_begin) * 64 + lane;
+    sp[si] = ps32 + (size_t)sc * G * 8 + (j >> 1);
+    zp[si] = pz + (size_t)sc * G * 2 + (j >> 3);
   }
-  auto load_b = [&](int c, u4 (&q)[S]) {
+  const int hsh = (j & 1) * 16;
+  const int zsh = (j & 7) * 4;
+
+  // ring slot: packed words plus, per group record, the scale and zero words
+  u4 qb[PB][S];
+  uint32_t sb[PB][S][GPC], zb[PB][S][GPC];
+  auto load_b = [&](int slot_u, int i) {  // i: chunk index within the split
+    const int c = c_begin + i;
 #pragma unroll
-    for (int si = 0; si < S; ++si)
-      q[si] = sval[si] ? __builtin_nontemporal_load(qp[si] + (size_t)c * 64) : u4{0u, 0u, 0u, 0u};
+    for (int si = 0; si < S; ++si) {
+      qb[slot_u][si] = __builtin_nontemporal_load(qp[si] + (size_t)i * 64);
+#pragma unroll
+      for (int gl = 0; gl < GPC; ++gl) {
+        const int g = GPC == 1 ? (c * kChunkK) / gs : c * GPC + gl;
+        sb[slot_u][si][gl] = sp[si][(size_t)g * 8];
+        zb[slot_u][si][gl] = zp[si][(size_t)g * 2];
+      }
+    }
   };
 
   f4 acc[MT2][S];
@@ -497,83 +487,200 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
     for (int si = 0; si < S; ++si) acc[mt][si] = f4{0.f, 0.f, 0.f, 0.f};
 
-  h8 areg[UNITS];
-  uint32_t mreg[MU];
-  u4 qcur[S], qnext[S];
-
-  if (c_begin < c_end) {
-    load_a(c_begin, areg);
-    load_m(c_begin, mreg);
-    load_b(c_begin, qcur);
-    store_a(0, areg);
-    store_m(0, mreg);
-  }
-  __syncthreads();
-
-  const int zsh = (j & 7) * 4;
   const uint32_t magic = kMagic;
-  for (int c = c_begin; c < c_end; ++c) {
-    const int buf = (c - c_begin) & 1;
-    const bool has_next = (c + 1) < c_end;
-    if (has_next) {
-      load_a(c + 1, areg);
-      load_m(c + 1, mreg);
-      load_b(c + 1, qnext);
-    }
-    const _Float16* Ab = &As[buf][0];
-    const uint32_t* Mb = &Ms[buf][0];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int gl = G128 ? 0 : (32 * t) / gs;
-      h8 bop[S];
-#pragma unroll
-      for (int si = 0; si < S; ++si) {
-        const uint32_t* mr = Mb + ((wave * S + si) * gpc + gl) * kMetaWords;
-        const _Float16 sc = reinterpret_cast<const _Float16*>(mr)[j];
-        h2 nz1024, nz64;
-        zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
-        const h8 d = centered8(qcur[si][t], nz1024, nz64, magic);
-        const h8 s8 = h8{sc, sc, sc, sc, sc, sc, sc, sc};
-        bop[si] = d * s8;  // fp16 product, round to nearest even
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT2; ++mt) {
-        const h8 a = *(const h8*)(Ab + (mt * 16 + j) * kLda + 32 * t + 8 * kq);
-#pragma unroll
-        for (int si = 0; si < S; ++si) acc[mt][si] = mfma16(a, bop[si], acc[mt][si]);
-      }
-    }
-    if (has_next) {
-      store_a(buf ^ 1, areg);
-      store_m(buf ^ 1, mreg);
-#pragma unroll
-      for (int si = 0; si < S; ++si) qcur[si] = qnext[si];
-    }
-    __syncthreads();
-  }
-
-  const bool direct = gridDim.y == 1;
-#pragma unroll
-  for (int mt = 0; mt < MT2; ++mt) {
+  // OCC == 1 (one workgroup per CU, one wave per SIMD): a wave has to hide
+  // its own latencies, so the four 32-row k-steps of a chunk are software
+  // pipelined -- while the MFMAs of step t run, the wave reads the A
+  // fragments of step t+1 from LDS and dequantises the B fragments of step
+  // t+1 (independent VALU work the scheduler interleaves with the MFMAs) --
+  // and activations are fetched two chunks ahead.
+  // OCC == 2 (two workgroups per CU, 256 registers per wave): the other
+  // wave on the SIMD overlaps its VALU and MFMA work with this one's, so the
+  // registers go to a plain schedule and a one-chunk activation prefetch.
+  constexpr bool PIPE = OCC == 1;
+  auto dequant = [&](int slot_u, int t, h8 (&bop)[S]) {
+    const int gl = GPC == 1 ? 0 : (t * GPC) / 4;
 #pragma unroll
     for (int si = 0; si < S; ++si) {
-      const int n = (strip0 + si) * kStripN + j;
+      h2 nz1024, nz64;
+      zero_consts(zb[slot_u][si][gl], zsh, nz1024, nz64);
+      const _Float16 sc = as_h((uint16_t)(sb[slot_u][si][gl] >> hsh));
+      const h8 d = centered8(qb[slot_u][si][t], nz1024, nz64, magic);
+      const h8 s8 = h8{sc, sc, sc, sc, sc, sc, sc, sc};
+      bop[si] = d * s8;  // fp16 product, round to nearest even
+    }
+  };
+  auto compute = [&](int slot_u, int buf) {
+    const _Float16* Ab = &As[buf][(size_t)j * kLda + 8 * kq];
+    if constexpr (PIPE) {
+      h8 af[2][MT2];
+      h8 bop[2][S];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + mt * 16 + kq * 4 + r;
-        if (m < M && sval[si]) {
-          const float v = acc[mt][si][r];
-          if (direct) {
-            _Float16 out = (_Float16)v;
-            if (bias != nullptr) out = out + as_h(bias[n]);
-            y[(size_t)m * ldy + n] = h_bits(out);
-          } else {
-            part[((size_t)split * M + m) * N + n] = v;
-          }
+      for (int mt = 0; mt < MT2; ++mt) af[0][mt] = *(const h8*)(Ab + mt * 16 * kLda);
+      dequant(slot_u, 0, bop[0]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t < 3) {
+#pragma unroll
+          for (int mt = 0; mt < MT2; ++mt)
+            af[(t + 1) & 1][mt] = *(const h8*)(Ab + mt * 16 * kLda + 32 * (t + 1));
+          dequant(slot_u, t + 1, bop[(t + 1) & 1]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+          for (int si = 0; si < S; ++si)
+            acc[mt][si] = mfma16(af[t & 1][mt], bop[t & 1][si], acc[mt][si]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        h8 bop[S];
+        dequant(slot_u, t, bop);
+#pragma unroll
+        for (int mt = 0; mt < MT2; ++mt) {
+          const h8 af = *(const h8*)(Ab + mt * 16 * kLda + 32 * t);
+#pragma unroll
+          for (int si = 0; si < S; ++si) acc[mt][si] = mfma16(af, bop[si], acc[mt][si]);
         }
       }
     }
+  };
+
+  // Activations travel global -> registers AD chunks ahead of their use and
+  // registers -> LDS one step ahead, so with AD == 2 a step only waits for
+  // loads issued a whole step earlier.  areg[i % AD] holds chunk i+AD while
+  // chunk i is computed (PB is even, so the parity is a compile-time index).
+  static_assert(PB % 2 == 0, "ring depth must be even");
+  constexpr int AD = PIPE ? 2 : 1;
+  h8 areg[AD][UNITS];
+  // prologue: ring filled with the first PB chunks (only those that exist
+  // when the split is shorter than the ring), chunk 0 in LDS, chunks
+  // 1..AD-1 in registers
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (u < nchunks) load_b(u, u);
+  if (nchunks > 0) {
+    load_a(c_begin, areg[0]);
+    store_a(0, areg[0]);
   }
+  if (AD == 2 && nchunks > 1) load_a(c_begin + 1, areg[AD - 1]);
+  __syncthreads();
+
+  // One step: fetch chunk i+AD's activations, compute chunk i from slot u,
+  // refill slot u with chunk i + PB, publish chunk i+1's activations.
+  auto step = [&](int u, int i, bool refill) {
+    const int p = u & 1;  // == i & 1
+    const int ra = AD == 2 ? p : 0;
+    const int rs = AD == 2 ? p ^ 1 : 0;
+    if (i + AD < nchunks) load_a(c_begin + i + AD, areg[ra]);
+    compute(u, p);
+    if (refill) load_b(u, i + PB);
+    if (i + 1 < nchunks) store_a(p ^ 1, areg[rs]);
+    __syncthreads();
+  };
+  int i0 = 0;
+  for (; i0 + 2 * PB <= nchunks; i0 += PB) {
+#pragma unroll
+    for (int u = 0; u < PB; ++u) step(u, i0 + u, true);
+  }
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (i0 + u < nchunks) step(u, i0 + u, i0 + u + PB < nchunks);
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (i0 + PB + u < nchunks) step(u, i0 + PB + u, false);
+
+  _Float16 bv[S];
+#pragma unroll
+  for (int si = 0; si < S; ++si)
+    bv[si] = (bias != nullptr && sval[si]) ? as_h(bias[(strip0 + si) * kStripN + j]) : (_Float16)0.f;
+  auto store_y = [&](int m, int n, int si, float v) {
+    _Float16 out = (_Float16)v;
+    if (bias != nullptr) out = out + bv[si];
+    y[(size_t)m * ldy + n] = h_bits(out);
+  };
+  const int splits = gridDim.y;
+  if (splits == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+      for (int si = 0; si < S; ++si)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + mt * 16 + kq * 4 + r;
+          if (m < M && sval[si]) store_y(m, (strip0 + si) * kStripN + j, si, acc[mt][si][r]);
+        }
+    return;
+  }
+
+  // Split-K: publish this split's fp32 partial tile, count the arrivals for
+  // the tile; the last split to arrive sums all partials in split order
+  // (deterministic whatever the arrival order), writes y and resets the
+  // counter for the next call.  No workgroup ever waits for another.
+  //
+  // Partials are kept in the accumulator's own register layout: for each
+  // (mt, si) fragment the workgroup writes 256 threads x 16 bytes
+  // contiguously (one float4 per thread, whole cache lines), in planes of
+  // mtiles*ntiles*BM*BN floats per split.  Ordering is the usual
+  // publish/consume pattern: the barrier orders every wave's stores before
+  // thread 0's agent-scope release fence and counter increment; the last
+  // arriver's acquire fence (then the barrier) orders the other splits'
+  // partials before its loads.  The fences run once per workgroup.
+  const int tile_id = mtile * ntiles + ntile;
+  f4* pt = reinterpret_cast<f4*>(part);
+  const size_t plane = (size_t)mtiles * ntiles * (MT2 * S) * 256;  // float4 per split
+  const size_t tbase = (size_t)tile_id * (MT2 * S) * 256 + tid;
+#pragma unroll
+  for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+    for (int si = 0; si < S; ++si)
+      pt[(size_t)split * plane + tbase + (mt * S + si) * 256] =
+          f4{acc[mt][si][0], acc[mt][si][1], acc[mt][si][2], acc[mt][si][3]};
+  __shared__ int last_arrival;
+  __syncthreads();
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == splits - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last_arrival = last;
+  }
+  __syncthreads();
+  if (!last_arrival) return;
+  // Sum in split order; per split all of this thread's loads are issued
+  // before any is used (one memory round trip per split).
+  f4 sum[MT2][S];
+#pragma unroll
+  for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+    for (int si = 0; si < S; ++si) sum[mt][si] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < splits; ++sp) {
+    f4 t[MT2][S];
+#pragma unroll
+    for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+      for (int si = 0; si < S; ++si)
+        t[mt][si] = sp == split ? f4{acc[mt][si][0], acc[mt][si][1], acc[mt][si][2], acc[mt][si][3]}
+                                : pt[(size_t)sp * plane + tbase + (mt * S + si) * 256];
+#pragma unroll
+    for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+      for (int si = 0; si < S; ++si) sum[mt][si] += t[mt][si];
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT2; ++mt)
+#pragma unroll
+    for (int si = 0; si < S; ++si)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + mt * 16 + kq * 4 + r;
+        if (m < M && sval[si]) store_y(m, (strip0 + si) * kStripN + j, si, sum[mt][si][r]);
+      }
+  if (tid == 0) __hip_atomic_store(&counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
@@ -722,8 +829,8 @@ hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hi
   }
 }
 
-template <int MT2, int S, bool ACT, bool G128>
-static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, float* part, hipStream_t stream) {
+template <int MT2, int S, int PB, int GPC, bool ACT, int OCC>
+static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
   constexpr int BM = 16 * MT2;
   constexpr int BN = 64 * S;
   const int mtiles = (a.M + BM - 1) / BM;
@@ -731,34 +838,42 @@ static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, float* part,
   const int KC = a.K / kChunkK;
   const int cps = (KC + splits - 1) / splits;
   const int real_splits = (KC + cps - 1) / cps;
+  if (real_splits > 1 && mtiles * ntiles > kSplitCounters) return hipErrorInvalidValue;
+  int* counters = static_cast<int*>(ws);
+  float* part = real_splits > 1
+                    ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
+                    : nullptr;
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
-  prefill_kernel<MT2, S, ACT, G128><<<grid, 256, 0, stream>>>(
+  prefill_kernel<MT2, S, PB, GPC, ACT, OCC><<<grid, 256, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
-      a.bias, a.y, a.ldy, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess || real_splits == 1) return err;
-  const size_t total = (size_t)a.M * a.N;
-  reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(part, real_splits, a.M, a.N,
-                                                                     a.bias, a.y, a.ldy);
+      a.bias, a.y, a.ldy, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   return hipGetLastError();
 }
 
-template <int MT2, int S>
-static hipError_t launch_prefill_tile(const GemmArgs& a, int splits, float* part, hipStream_t stream) {
+template <int MT2, int S, int PB, int OCC>
+static hipError_t launch_prefill_tile(const GemmArgs& a, int splits, void* part, hipStream_t stream) {
   const bool act = a.perm != nullptr;
-  const bool g128 = (a.gs % kChunkK) == 0;
-  if (act) {
-    return g128 ? launch_prefill_cfg<MT2, S, true, true>(a, splits, part, stream)
-                : launch_prefill_cfg<MT2, S, true, false>(a, splits, part, stream);
-  }
-  return g128 ? launch_prefill_cfg<MT2, S, false, true>(a, splits, part, stream)
-              : launch_prefill_cfg<MT2, S, false, false>(a, splits, part, stream);
+  const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
+#define DW4_PREFILL_G(GG)                                                               \
+  return act ? launch_prefill_cfg<MT2, S, PB, GG, true, OCC>(a, splits, part, stream)    \
+             : launch_prefill_cfg<MT2, S, PB, GG, false, OCC>(a, splits, part, stream)
+  if (gpc == 1) { DW4_PREFILL_G(1); }
+  if (gpc == 2) { DW4_PREFILL_G(2); }
+  DW4_PREFILL_G(4);
+#undef DW4_PREFILL_G
 }
 
-hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, float* part, hipStream_t stream) {
-  if (plan.bm == 64 && plan.bn == 128) return launch_prefill_tile<4, 2>(a, plan.splits, part, stream);
-  if (plan.bm == 128 && plan.bn == 128) return launch_prefill_tile<8, 2>(a, plan.splits, part, stream);
-  if (plan.bm == 64 && plan.bn == 64) return launch_prefill_tile<4, 1>(a, plan.splits, part, stream);
+hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* part, hipStream_t stream) {
+  // Four strips per wave (BN = 256) give each LDS activation read four MFMA
+  // uses; measured LDS bandwidth (~128 B/clk/CU) makes two strips per wave
+  // LDS-bound.  The register ring is shallower for the wider tiles.
+  if (plan.bm == 64 && plan.bn == 256) {
+    if (plan.occ == 2) return launch_prefill_tile<4, 4, 2, 2>(a, plan.splits, part, stream);
+    return launch_prefill_tile<4, 4, DW4_PREFILL_PB, 1>(a, plan.splits, part, stream);
+  }
+  if (plan.bm == 128 && plan.bn == 256) return launch_prefill_tile<8, 4, 2, 1>(a, plan.splits, part, stream);
+  if (plan.bm == 64 && plan.bn == 128) return launch_prefill_tile<4, 2, 4, 1>(a, plan.splits, part, stream);
+  if (plan.bm == 128 && plan.bn == 128) return launch_prefill_tile<8, 2, 4, 1>(a, plan.splits, part, stream);
   return hipErrorInvalidValue;
 }
 

@@ -68,8 +68,10 @@ class CacheV2(object):
             self._temp_weight = None
 
     def init_cache(self) -> None:
-        # at least 16 bytes so the pointer is never null and always aligned
-        self._workspace = torch.empty(max(self.workspace_size, 16), dtype=torch.uint8,
+        # Zero-filled once: its head holds split-K arrival counters that the
+        # library expects at zero and leaves at zero after every call.  At
+        # least 16 bytes so the pointer is never null and always aligned.
+        self._workspace = torch.zeros(max(self.workspace_size, 16), dtype=torch.uint8,
                                       device=self.device)
         self.cache_created = True
 

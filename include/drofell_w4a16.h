@@ -27,9 +27,15 @@
  *     is a hipStream_t (NULL = the null stream).  Work is enqueued on it.
  *   - dw4_gemm never synchronises, never allocates and launches a fixed
  *     sequence of kernels for a given (m, k, n, workspace) so it may be
- *     captured into a HIP graph.  Its result is deterministic (no atomics).
+ *     captured into a HIP graph.  Its result is deterministic: split-K
+ *     partial sums are always added in split order, whatever order the
+ *     workgroups finish in.
  *   - dw4_make_perm runs on the host; dw4_repack may be called once per
  *     load or swap-in and does not synchronise either.
+ *   - The dw4_gemm workspace must be zero-filled before its first use; the
+ *     library keeps split-K arrival counters at its start and leaves them at
+ *     zero after every call.  Calls that overlap in time on one workspace
+ *     race (give concurrent streams their own workspace).
  *
  * Shapes (GPTQ checkpoint format, the module buffers of QuantLinear,
  * operators/core/linear/real_quant.py:10-49 in the reference):
@@ -40,9 +46,10 @@
  *   g_idx   int32 [K]        group of each row (act-order only)
  *   x fp16 [M, K] (row stride ldx), y fp16 [M, N] (row stride ldy)
  *   G = K / group_size.
- * Supported: K % 128 == 0, N % 16 == 0, group_size % 32 == 0 (or
- * group_size == K), K % group_size == 0; act-order requires every group to
- * hold exactly group_size rows (what GPTQ desc_act produces).
+ * Supported: K % 128 == 0, N % 16 == 0, group_size in {32, 64} or a
+ * multiple of 128 (group_size == K included), K % group_size == 0;
+ * act-order requires every group to hold exactly group_size rows (what GPTQ
+ * desc_act produces).
  *
  * Packed layout written by dw4_repack (same byte counts as the inputs, so
  * a module keeps its buffer sizes):

@@ -107,10 +107,14 @@ def test_workspace_size_rules():
     # act-order gathers while staging: no gather buffer
     assert _lib.workspace_size(8, 4096, 4096, 128, True) == _lib.workspace_size(8, 4096, 4096, 128, False)
     # M=16 x K=11008 does not fit one workgroup's LDS: fp32 split-K planes
+    # a split call's workspace: a fixed 16 KiB head of arrival counters, then
+    # whole fp32 partial planes [splits][M][N]
+    head = 4096 * 4
     ws = _lib.workspace_size(16, 11008, 4096, 128, False)
-    assert ws > 0 and ws % (16 * 4096 * 4) == 0
+    assert ws > head and (ws - head) % (16 * 4096 * 4) == 0
     ws = _lib.workspace_size(256, 4096, 4096, 128, False)
-    assert ws % (256 * 4096 * 4) == 0  # whole fp32 split-K partial planes
+    plane = 256 * 4096 * 4
+    assert ws > head + plane and (ws - head) % plane == 0
 
 
 def test_quantlinear_buffers_match_reference_layout():

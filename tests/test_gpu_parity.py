@@ -222,6 +222,36 @@ def test_prefill_large_m_and_split_k(hip_device):
         check_tol(y, ref, f"M=2048 split {split}")
 
 
+def test_shared_workspace_across_shapes(hip_device):
+    """Two matrices share one workspace; decode split-K partials and prefill
+    split-K calls of different tile counts alternate on it.  Each result
+    stays within tolerance and the arrival counters at the head of the
+    workspace are all zero after every call."""
+    cache = CacheV2(hip_device)
+    mats = {}
+    for k, n in ((11008, 4096), (4096, 11008)):
+        lay, w = oracle_w(k, n, 128, 1002 + k, False, False)
+        d = lay.to(hip_device)
+        mats[(k, n)] = (Q4MatrixV2(d.qweight, d.qzeros, d.scales, k, n, None, False,
+                                   TuningParams(MAX_M=512), cache), w)
+    cache.init_cache()
+    head = 4096  # int32 arrival counters
+    seq = [((11008, 4096), 16, _lib.DW4_PATH_DECODE, 0), ((4096, 11008), 100, _lib.DW4_PATH_PREFILL, 0),
+           ((11008, 4096), 64, _lib.DW4_PATH_PREFILL, 0), ((4096, 11008), 16, _lib.DW4_PATH_PREFILL, 5),
+           ((11008, 4096), 16, _lib.DW4_PATH_DECODE, 0), ((4096, 11008), 130, _lib.DW4_PATH_PREFILL, 2),
+           ((4096, 11008), 100, _lib.DW4_PATH_PREFILL, 0)]
+    for (k, n), m, path, split in seq:
+        say(f"shared workspace {k}x{n} M={m} path={path} split={split}")
+        q4, w = mats[(k, n)]
+        q4.tuning_params = TuningParams(MAX_M=512, PREFILL_SPLIT_K=split)
+        x = make_x(m, k, seed=m + k)
+        y = q4.matmul(x.to(hip_device), path=path)
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"shared ws {k}x{n} M={m} path {path}")
+        counters = cache.workspace[: head * 4].view(torch.int32)
+        assert int(torch.count_nonzero(counters)) == 0
+
+
 def test_deterministic(hip_device):
     lay, _ = oracle_w(4096, 11008, 128, 1001, False, False)
     q4 = build(lay, hip_device)
@@ -275,10 +305,10 @@ def test_errors_surface(hip_device):
                       q4.scales.data_ptr(), None, None, y.data_ptr(), 4096, None, 0, None)
     assert st == _lib.DW4_ERR_UNSUPPORTED
     say("errors: split decode without workspace")
-    # M=16 x K=4096 activations exceed one workgroup's LDS: fp32 split-K partials needed
-    xs = torch.zeros(16, 4096, dtype=torch.float16, device=hip_device)
-    ys = torch.empty(16, 4096, dtype=torch.float16, device=hip_device)
-    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 16, 4096, 4096, 128, xs.data_ptr(), 4096,
+    # M=64 x K=4096 activations exceed one workgroup's LDS: fp32 split-K partials needed
+    xs = torch.zeros(64, 4096, dtype=torch.float16, device=hip_device)
+    ys = torch.empty(64, 4096, dtype=torch.float16, device=hip_device)
+    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 64, 4096, 4096, 128, xs.data_ptr(), 4096,
                            q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(), None,
                            None, ys.data_ptr(), 4096, None, 0, None)
     assert st == _lib.DW4_ERR_WORKSPACE
