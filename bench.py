@@ -160,6 +160,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run 5 plain device copies of this many bytes (the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -172,6 +175,14 @@ def main() -> int:
     from gptq_synth import LLAMA2_7B_SHAPES, algorithmic_bytes, flops
 
     dev = torch.device("cuda", 0)
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        log(f"copied {args.copy_bytes} bytes 5 times")
+        return 0
     log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
     mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1024 if args.sweep else 1))
     weight_bytes = sum(q4.qweight.numel() * 4 + q4.scales.numel() * 2 + q4.qzeros.numel() * 4
@@ -205,6 +216,9 @@ def main() -> int:
             "weight_bytes": weight_bytes, "algorithmic_bytes_per_step": step_bytes,
             "launches_per_step": len(mats), "hip_graph": True,
         },
+        # Dominant (only) kernel of the step: dw4::decode_kernel.  Algorithmic
+        # bytes per launch (mean over the 56 launches) / mean launch duration
+        # (HIP events around the graph replays on the replay stream / 56).
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),
@@ -212,6 +226,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
+            "kernel": "dw4::decode_kernel",
+            "bytes_per_launch": step_bytes // len(mats),
+            "avg_launch_us": round(ms * 1e3 / len(mats), 3),
         },
     }
 

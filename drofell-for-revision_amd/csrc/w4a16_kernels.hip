@@ -6,7 +6,7 @@
 // reconstruct + cuBLAS) and the Marlin repack/GEMM.  Layouts and names of
 // the packed buffers are documented in include/drofell_w4a16.h.
 //
-// Arithmetic contract (reference: operators/core/linear/real_quant.py:97-118)
+// Arithmetic contract (reference: operators/core/linear/real_quant.py:69-102)
 //   W[k,n] = fp16_rne(scale[g(k),n] * (q[k,n] - (zero[g(k),n] + 1)))
 //   y[m,n] = fp16_rne(sum_k x[m,k] * W[k,n])  (fp32 accumulation)
 // The decode kernel factors the scale out of each group (fp32 products of

@@ -186,20 +186,45 @@ class Q4MatrixV2(object):
         return _lib.DW4_PATH_PREFILL
 
     def matmul(self, x: torch.Tensor, output: Optional[torch.Tensor] = None,
+               temp_weight: Optional[torch.Tensor] = None, must_blas: bool = False, *,
                bias: Optional[torch.Tensor] = None, path: Optional[int] = None) -> torch.Tensor:
-        """``x @ W (+ bias)`` for x [..., K]; fp16 compute, x's dtype out."""
+        """``x @ W (+ bias)`` for x [..., K] in x's dtype (fp16 or bf16).
+
+        Same arguments as the reference (``exllama.py:492-526``): with a
+        reconstructed fp16 weight, or ``must_blas``, the product is the dense
+        one over the dequantised weight (bit-exact HIP dequantisation into
+        ``temp_weight`` or the shared buffer, then a library GEMM); otherwise
+        the HIP W4A16 kernel runs (decode kernel for small M, MFMA prefill
+        kernel above).  bf16 activations are rounded to fp16 for the
+        product.  ``bias`` (fp16 [N]) is added after the fp16 rounding of
+        the product, as ``output += bias`` does in the reference.
+        """
         if x.device != self.device:
             raise ValueError(f"input on {x.device}, weights on {self.device}")
+        if x.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
         in_dtype = x.dtype
         if in_dtype != torch.float16:
             x = x.to(torch.float16)
         outshape = x.shape[:-1] + (self.width,)
         x2 = _aligned_rows(x.reshape(-1, self.height))
         m = x2.shape[0]
-        if output is None or output.dtype != torch.float16 or not output.is_contiguous():
-            output = torch.empty((m, self.width), dtype=torch.float16, device=self.device)
         if bias is not None:
             bias = bias.to(torch.float16).contiguous()
+        if must_blas or self.reconstructed_weight_float16 is not None:
+            w = self.reconstructed_weight_float16
+            if w is None:
+                w = self._dense_weight(temp_weight)
+            y = torch.matmul(x2, w)
+            if bias is not None:
+                y += bias
+            if output is not None:
+                output.view(m, self.width).copy_(y)
+                y = output
+            y = y.view(outshape)
+            return y if in_dtype == torch.float16 else y.to(in_dtype)
+        if output is None or output.dtype != torch.float16 or not output.is_contiguous():
+            output = torch.empty((m, self.width), dtype=torch.float16, device=self.device)
         ws = self.cache.workspace
         lib = _lib.load()
         status = lib.dw4_gemm_path(
@@ -213,6 +238,15 @@ class Q4MatrixV2(object):
         _lib.check("dw4_gemm_path", status)
         out = output.view(outshape)
         return out if in_dtype == torch.float16 else out.to(in_dtype)
+
+    def _dense_weight(self, temp_weight: Optional[torch.Tensor]) -> torch.Tensor:
+        """The fp16 [K, N] weight dequantised into ``temp_weight`` (or the
+        shared per-device buffer)."""
+        buf = temp_weight if temp_weight is not None else self.cache.temp_weight
+        if buf.dtype != torch.float16 or buf.numel() < self.height * self.width:
+            raise ValueError("temp_weight must be an fp16 buffer of at least K*N elements")
+        w = buf.view(-1)[: self.height * self.width].view(self.height, self.width)
+        return self.get_float16_weights_matrix_v2(w)
 
     def get_float16_weights_matrix_v2(self, out_matrix: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Dequantised fp16 weight [K, N] in the checkpoint's row order."""
@@ -235,22 +269,35 @@ class Q4MatrixV2(object):
     def release_weight(self, dtype: Optional[torch.dtype] = None) -> None:
         self.reconstructed_weight_float16 = None
 
-    def transpose_matmul(self, x: torch.Tensor, weight: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def transpose_matmul(self, x: torch.Tensor, output: Optional[torch.Tensor] = None,
+                         temp_weight: Optional[torch.Tensor] = None,
+                         skip_reconstruct: bool = False) -> torch.Tensor:
         """``x @ W.T`` for x [..., N] (the activation gradient of the forward).
 
-        The weight is dequantised bit-exactly by the HIP kernel (into the
-        shared temp buffer unless a cached weight is given); the dense
-        product is a plain library GEMM.
+        Same arguments as the reference (``exllama.py:528-544``): the weight
+        is the reconstructed one if present, else it is dequantised
+        bit-exactly into ``temp_weight`` (or the shared buffer) -- skipped
+        with ``skip_reconstruct`` when the caller already filled it -- and
+        the dense product is a plain library GEMM.
         """
-        if weight is None:
-            weight = self.reconstructed_weight_float16
-        if weight is None:
-            weight = self.cache.temp_weight.view(-1)[: self.height * self.width].view(
-                self.height, self.width)
-            self.get_float16_weights_matrix_v2(weight)
+        if x.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
+        w = self.reconstructed_weight_float16
+        if w is None:
+            if skip_reconstruct:
+                if temp_weight is None:
+                    raise ValueError("skip_reconstruct needs the filled temp_weight")
+                w = temp_weight.view(-1)[: self.height * self.width].view(self.height, self.width)
+            else:
+                w = self._dense_weight(temp_weight)
         in_dtype = x.dtype
-        out = torch.matmul(x.to(torch.float16), weight.t())
-        return out if in_dtype == torch.float16 else out.to(in_dtype)
+        outshape = x.shape[:-1] + (self.height,)
+        y = torch.matmul(x.reshape(-1, self.width).to(torch.float16), w.t())
+        if output is not None:
+            output.view(-1, self.height).copy_(y)
+            y = output
+        y = y.view(outshape)
+        return y if in_dtype == torch.float16 else y.to(in_dtype)
 
 
 class Q4LinearFunction(Function):
@@ -273,8 +320,11 @@ class Q4LinearFunction(Function):
     def backward(ctx: Any, grad_output: torch.Tensor):  # type: ignore[override]
         grad_input = None
         if ctx.needs_input_grad[0]:
-            weight = ctx.saved_tensors[0] if ctx.has_cached else None
-            grad_input = ctx.weight_q4.transpose_matmul(grad_output, weight)
+            if ctx.has_cached:
+                grad_input = ctx.weight_q4.transpose_matmul(
+                    grad_output, None, ctx.saved_tensors[0], skip_reconstruct=True)
+            else:
+                grad_input = ctx.weight_q4.transpose_matmul(grad_output)
         return grad_input, None, None, None
 
 

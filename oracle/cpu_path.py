@@ -17,7 +17,7 @@ _WF = torch.arange(0, 32, 4, dtype=torch.int32)
 
 def reconstruct_weights(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
                         g_idx: torch.Tensor) -> torch.Tensor:
-    """fp16 [K, N]: torch shift/and/gather/fp16-multiply, as real_quant.py:97-118."""
+    """fp16 [K, N]: torch shift/and/gather/fp16-multiply, as real_quant.py:69-102."""
     zeros = torch.bitwise_right_shift(qzeros.unsqueeze(2).expand(-1, -1, 8),
                                       _WF.unsqueeze(0)).to(torch.int8)
     torch.bitwise_and(zeros, 15, out=zeros)

@@ -10,15 +10,15 @@ It restates, in numpy, the arithmetic the reference defines for one GPTQ
 
 * nibble addressing of ``qweight`` (rows packed along K) --
   ``cuda_extends/exllama/matrix.cuh:156-160`` (``MatrixView_q4_column``),
-  ``operators/core/linear/real_quant.py:107-114``;
+  ``operators/core/linear/real_quant.py:79-86``;
 * nibble addressing of ``qzeros`` (columns packed along N) --
   ``cuda_extends/exllama/matrix.cuh:120-124`` (``MatrixView_q4_row``),
-  ``operators/core/linear/real_quant.py:98-105``;
-* the "+1" effective zero -- ``real_quant.py:104``,
+  ``operators/core/linear/real_quant.py:70-77``;
+* the "+1" effective zero -- ``real_quant.py:76``,
   ``cuda_extends/exllama/q4_matrix.cu:221``,
   ``cuda_extends/exllama/q_gemm_kernel_gptq.cuh:131-134``;
 * the dequantised weight ``W[k,n] = fp16(scales[g_idx[k],n] *
-  (q[k,n] - z[g_idx[k],n]))`` -- ``real_quant.py:115-118``
+  (q[k,n] - z[g_idx[k],n]))`` -- ``real_quant.py:89-90``
   (``QuantLinear.get_reconstruct_weights``; the GPU kernels compute the
   same value: ``q4_matrix.cu:418,427`` and
   ``cuda_extends/marlin/marlin_dequant.cu:72``);
@@ -90,7 +90,7 @@ def pack_qzeros(z: np.ndarray) -> np.ndarray:
 
 
 def default_g_idx(k: int, group_size: int) -> np.ndarray:
-    """``g_idx[k] = k // group_size`` (``real_quant.py:68-72``)."""
+    """``g_idx[k] = k // group_size`` (``real_quant.py:40-44``)."""
     return (np.arange(k) // group_size).astype(np.int32)
 
 
@@ -99,7 +99,7 @@ def dequantize(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray,
     """fp16 [K, N] weight in ORIGINAL row order.
 
     ``W[k,n] = fp16_rne(scales[g_idx[k], n] * (q[k,n] - (z[g_idx[k], n] + 1)))``
-    -- ``real_quant.py:97-118``.  The integer difference is exact and
+    -- ``real_quant.py:69-102``.  The integer difference is exact and
     |q - z| <= 16, so the fp32 product of an fp16 scale and it is exact; the
     single rounding is the fp32 -> fp16 round-to-nearest-even, which is what
     an fp16 multiply produces (``q4_matrix.cu:418``, ``__hmul2``).

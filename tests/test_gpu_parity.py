@@ -252,6 +252,59 @@ def test_shared_workspace_across_shapes(hip_device):
         assert int(torch.count_nonzero(counters)) == 0
 
 
+def test_operator_routes(hip_device):
+    """QuantLinear end to end through every route the reference has:
+    no-grad forward (HIP kernel), bias, bf16 activations, must_blas and
+    reconstructed-weight dense products, and the input gradient of the
+    grad-enabled forward (x @ W.T through the dequantised weight)."""
+    from operators.core.linear.real_quant import QuantLinearMaker
+    k, n = 1024, 512
+    lay, w = oracle_w(k, n, 128, 4242, False, True)
+    maker = QuantLinearMaker(quantization_group_size=128, use_act_order=True)
+    with torch.device(hip_device):
+        lin = maker.make_linear(k, n, bias=True)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.5).half()
+    lin.load_state_dict({"qweight": lay.qweight, "qzeros": lay.qzeros, "scales": lay.scales,
+                         "g_idx": lay.g_idx, "bias": bias})
+    cache = CacheV2(hip_device)
+    maker.post_init(TuningParams(), cache)
+    cache.init_cache()
+    q4 = lin.q4_matrix
+    x = make_x(24, k, seed=77)
+    ref = gptq.gemm_ref(x.numpy(), w) + bias.float().numpy()
+    xd = x.to(hip_device)
+    say("operator: no-grad forward with bias")
+    y = lin(xd.view(2, 12, k))
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (2, 12, n) and y.dtype == torch.float16
+    check_tol(y.reshape(24, n), ref, "forward + bias")
+    say("operator: bf16 activations")
+    yb = lin(xd.to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert yb.dtype == torch.bfloat16
+    check_tol(yb.float(), gptq.gemm_ref(x.to(torch.bfloat16).half().numpy(), w)
+              + bias.float().numpy(), "bf16 forward")
+    say("operator: must_blas dense route")
+    yd = q4.matmul(xd, None, None, True, bias=bias.to(hip_device))
+    torch.cuda.synchronize()
+    check_tol(yd, ref, "must_blas")
+    say("operator: reconstructed weight route")
+    q4.reconstruct_weight(torch.float16)
+    yr = lin(xd)
+    q4.release_weight()
+    torch.cuda.synchronize()
+    check_tol(yr, ref, "reconstructed")
+    say("operator: input gradient")
+    xg = xd.clone().requires_grad_(True)
+    yg = lin(xg)
+    g = make_x(24, n, seed=78)
+    yg.backward(g.to(hip_device))
+    torch.cuda.synchronize()
+    check_tol(yg.detach(), ref, "grad-enabled forward")
+    gref = g.numpy().astype(np.float64) @ w.astype(np.float64).T
+    check_tol(xg.grad, gref, "input gradient")
+
+
 def test_deterministic(hip_device):
     lay, _ = oracle_w(4096, 11008, 128, 1001, False, False)
     q4 = build(lay, hip_device)
