@@ -51,9 +51,13 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n);
 // split count: with too little workspace the call runs unsplit.
 dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_bytes, bool cap_by_ws) {
   dw4::PrefillPlan p;
-  p.bm = m <= 512 ? 64 : 128;
+  p.bm = m < DW4_PREFILL_BM128_MIN_M ? 64 : 128;
   p.bn = n >= 2048 ? 256 : 128;
   p.occ = (p.bm == 64 && p.bn == 256) ? DW4_PREFILL_OCC : 1;
+  if (DW4_PREFILL_NARROW128 && p.bm == 128) {  // 128x128 tiles, two workgroups per CU
+    p.bn = 128;
+    p.occ = 2;
+  }
   const int kc = k / kChunkK;
   const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
   int splits = split_req;

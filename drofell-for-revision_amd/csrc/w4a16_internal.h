@@ -20,6 +20,12 @@ constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 #ifndef DW4_PREFILL_PB
 #define DW4_PREFILL_PB 4  // prefill weight ring depth (chunks) of the 64x256 tile
 #endif
+#ifndef DW4_PREFILL_BM128_MIN_M
+#define DW4_PREFILL_BM128_MIN_M 513  // smallest M that gets 128-row prefill tiles
+#endif
+#ifndef DW4_PREFILL_NARROW128
+#define DW4_PREFILL_NARROW128 0  // 128-row tiles use 128 columns and two workgroups per CU
+#endif
 #ifndef DW4_PREFILL_OCC
 #define DW4_PREFILL_OCC 1  // workgroups per CU of the 64x256 prefill tile
 #endif

@@ -597,22 +597,56 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
   for (int si = 0; si < S; ++si)
     bv[si] = (bias != nullptr && sval[si]) ? as_h(bias[(strip0 + si) * kStripN + j]) : (_Float16)0.f;
-  auto store_y = [&](int m, int n, int si, float v) {
-    _Float16 out = (_Float16)v;
-    if (bias != nullptr) out = out + bv[si];
-    y[(size_t)m * ldy + n] = h_bits(out);
-  };
-  const int splits = gridDim.y;
-  if (splits == 1) {
+  // Output: the accumulator layout gives a lane four rows of one column, so
+  // direct stores would be 2-byte stores, which the address unit processes
+  // about one lane per cycle (~7 us per workgroup for a 64x256 tile).  Each
+  // wave instead rounds its (16*MT2) x (16*S) tile to fp16 (adding the bias
+  // after the rounding, like `y += bias` on an fp16 tensor), writes it in
+  // row order to its own slice of the now idle activation buffers, and
+  // stores whole 16-byte row segments.  Every caller has passed the last
+  // barrier of the main loop, so no wave still reads the activations.
+  constexpr int TW = 16 * S;       // tile width in halves
+  constexpr int SEG = TW / 8;      // 16-byte segments per tile row
+  constexpr int RPP = 64 / SEG;    // tile rows per 64-lane pass
+  static_assert(4 * 16 * MT2 * TW <= 2 * BM * kLda, "output tiles fit in the activation buffers");
+  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0);
+  auto write_tile = [&](auto&& val) {  // val(mt, si, r): fp32 result of that accumulator slot
+    _Float16* T = &As[0][0] + wave * (16 * MT2 * TW);
 #pragma unroll
     for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
       for (int si = 0; si < S; ++si)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = m0 + mt * 16 + kq * 4 + r;
-          if (m < M && sval[si]) store_y(m, (strip0 + si) * kStripN + j, si, acc[mt][si][r]);
+          _Float16 out = (_Float16)val(mt, si, r);
+          if (bias != nullptr) out = out + bv[si];
+          T[(mt * 16 + kq * 4 + r) * TW + si * 16 + j] = out;
         }
+    __syncthreads();
+#pragma unroll
+    for (int pass = 0; pass < 16 * MT2 / RPP; ++pass) {
+      const int row = pass * RPP + lane / SEG;
+      const int seg = lane % SEG;
+      const int m = m0 + row;
+      const int strip = strip0 + seg / 2;
+      if (m < M && strip < NS) {
+        const u4 v = *(const u4*)&T[row * TW + seg * 8];
+        uint16_t* dst = y + (size_t)m * ldy + strip * kStripN + (seg & 1) * 8;
+        if (vec_y) {
+          *(u4*)dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dst[2 * e] = (uint16_t)(v[e] & 0xFFFFu);
+            dst[2 * e + 1] = (uint16_t)(v[e] >> 16);
+          }
+        }
+      }
+    }
+  };
+  const int splits = gridDim.y;
+  if (splits == 1) {
+    write_tile([&](int mt, int si, int r) { return acc[mt][si][r]; });
     return;
   }
 
@@ -621,29 +655,32 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   // (deterministic whatever the arrival order), writes y and resets the
   // counter for the next call.  No workgroup ever waits for another.
   //
-  // Partials are kept in the accumulator's own register layout: for each
-  // (mt, si) fragment the workgroup writes 256 threads x 16 bytes
-  // contiguously (one float4 per thread, whole cache lines), in planes of
-  // mtiles*ntiles*BM*BN floats per split.  Ordering is the usual
-  // publish/consume pattern: the barrier orders every wave's stores before
-  // thread 0's agent-scope release fence and counter increment; the last
-  // arriver's acquire fence (then the barrier) orders the other splits'
-  // partials before its loads.  The fences run once per workgroup.
+  // Partials are written as relaxed agent-scope atomic stores, which gfx950
+  // performs write-through (sc1): they leave no dirty L2 lines, so thread
+  // 0's agent-scope release -- an L2 write-back -- has almost nothing to
+  // write (with plain stores it had to flush every workgroup's partials and
+  // cost several microseconds).  Layout per split plane (mtiles*ntiles*BM*BN
+  // floats): [tile][mt*S + si][element e of the lane's float4][256 threads],
+  // so each store instruction covers 256 contiguous bytes per wave.
+  // Ordering is the usual publish/consume pattern: the barrier orders every
+  // wave's stores before thread 0's release and counter increment; the last
+  // arriver's acquire (then the barrier) orders the other splits' partials
+  // before its loads.  Fences run once per workgroup.
   const int tile_id = mtile * ntiles + ntile;
-  f4* pt = reinterpret_cast<f4*>(part);
-  const size_t plane = (size_t)mtiles * ntiles * (MT2 * S) * 256;  // float4 per split
-  const size_t tbase = (size_t)tile_id * (MT2 * S) * 256 + tid;
+  const size_t plane = (size_t)mtiles * ntiles * (MT2 * S) * 1024;  // floats per split
+  const size_t tbase = (size_t)tile_id * (MT2 * S) * 1024 + tid;
 #pragma unroll
   for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
     for (int si = 0; si < S; ++si)
-      pt[(size_t)split * plane + tbase + (mt * S + si) * 256] =
-          f4{acc[mt][si][0], acc[mt][si][1], acc[mt][si][2], acc[mt][si][3]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        __hip_atomic_store(&part[(size_t)split * plane + tbase + (mt * S + si) * 1024 + e * 256],
+                           acc[mt][si][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __shared__ int last_arrival;
   __syncthreads();
   if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELAXED,
+    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELEASE,
                                               __HIP_MEMORY_SCOPE_AGENT);
     const int last = before == splits - 1;
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -663,23 +700,17 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
     for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
-      for (int si = 0; si < S; ++si)
+      for (int si = 0; si < S; ++si) {
+        const float* src = part + (size_t)sp * plane + tbase + (mt * S + si) * 1024;
         t[mt][si] = sp == split ? f4{acc[mt][si][0], acc[mt][si][1], acc[mt][si][2], acc[mt][si][3]}
-                                : pt[(size_t)sp * plane + tbase + (mt * S + si) * 256];
+                                : f4{src[0], src[256], src[512], src[768]};
+      }
 #pragma unroll
     for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
       for (int si = 0; si < S; ++si) sum[mt][si] += t[mt][si];
   }
-#pragma unroll
-  for (int mt = 0; mt < MT2; ++mt)
-#pragma unroll
-    for (int si = 0; si < S; ++si)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + mt * 16 + kq * 4 + r;
-        if (m < M && sval[si]) store_y(m, (strip0 + si) * kStripN + j, si, sum[mt][si][r]);
-      }
+  write_tile([&](int mt, int si, int r) { return sum[mt][si][r]; });
   if (tid == 0) __hip_atomic_store(&counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -873,7 +904,10 @@ hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* part
   }
   if (plan.bm == 128 && plan.bn == 256) return launch_prefill_tile<8, 4, 2, 1>(a, plan.splits, part, stream);
   if (plan.bm == 64 && plan.bn == 128) return launch_prefill_tile<4, 2, 4, 1>(a, plan.splits, part, stream);
-  if (plan.bm == 128 && plan.bn == 128) return launch_prefill_tile<8, 2, 4, 1>(a, plan.splits, part, stream);
+  if (plan.bm == 128 && plan.bn == 128) {
+    if (plan.occ == 2) return launch_prefill_tile<8, 2, 2, 2>(a, plan.splits, part, stream);
+    return launch_prefill_tile<8, 2, 4, 1>(a, plan.splits, part, stream);
+  }
   return hipErrorInvalidValue;
 }
 

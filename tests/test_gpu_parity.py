@@ -305,6 +305,30 @@ def test_operator_routes(hip_device):
     check_tol(xg.grad, gref, "input gradient")
 
 
+def test_unaligned_output_rows(hip_device):
+    """y at an odd element offset with a row stride that is not a multiple
+    of 8 halves (no 16-byte row segments): same bits as an aligned y."""
+    lay, w = oracle_w(4096, 4096, 128, 1000, False, False)
+    q4 = build(lay, hip_device)
+    lib = _lib.load()
+    ws = q4.cache.workspace
+    for m, path in ((3, _lib.DW4_PATH_DECODE), (40, _lib.DW4_PATH_PREFILL),
+                    (256, _lib.DW4_PATH_PREFILL)):
+        say(f"unaligned y M={m} path={path}")
+        x = make_x(m, 4096, seed=m + 500).to(hip_device)
+        ref = q4.matmul(x, path=path)
+        big = torch.full((m * 4100 + 8,), -1, dtype=torch.int16, device=hip_device)
+        yv = big[1:1 + m * 4100].view(m, 4100)
+        st = lib.dw4_gemm_path(path, 0, m, 4096, 4096, 128, x.data_ptr(), 4096,
+                               q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(),
+                               None, None, yv.data_ptr(), 4100, ws.data_ptr(), ws.numel(),
+                               torch.cuda.current_stream().cuda_stream)
+        assert st == _lib.DW4_OK
+        torch.cuda.synchronize()
+        assert torch.equal(yv[:, :4096], ref.view(torch.int16))
+        assert bool((yv[:, 4096:] == -1).all()) and int(big[0]) == -1
+
+
 def test_deterministic(hip_device):
     lay, _ = oracle_w(4096, 11008, 128, 1001, False, False)
     q4 = build(lay, hip_device)
