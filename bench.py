@@ -37,7 +37,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234):
+def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None):
     import torch
     from gptq_synth import LLAMA2_7B_SHAPES
     from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
@@ -47,7 +47,7 @@ def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234):
     gen = torch.Generator(device=dev)
     mats = []
     for layer in range(layers):
-        for pi, (name, (k, n)) in enumerate(LLAMA2_7B_SHAPES.items()):
+        for pi, (name, (k, n)) in enumerate((shapes or LLAMA2_7B_SHAPES).items()):
             gen.manual_seed(seed0 + 100 * layer + pi)
             groups = k // GROUP
             # uniform random words == every nibble uniform in 0..15
@@ -134,9 +134,10 @@ def cpu_baseline(seconds: float) -> dict:
                        f"median {med * 1e3:.1f} ms; torch {torch.__version__}")}
 
 
-def sweep(mats, dev, steps: int, warmup: int) -> None:
+def sweep(mats, dev, steps: int, warmup: int,
+          shapes=((4096, 4096), (4096, 11008), (11008, 4096))) -> None:
     from gptq_synth import algorithmic_bytes, flops
-    for (k, n) in ((4096, 4096), (4096, 11008), (11008, 4096)):
+    for (k, n) in shapes:
         for m in (1, 2, 4, 8, 16, 64, 256, 1024):
             ms, _, sel = time_graph(mats, m, steps, warmup, dev,
                                     select=lambda t, k=k, n=n: t[1] == k and t[2] == n)
@@ -159,6 +160,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-merged", action="store_true",
+                    help="skip the merged-projection (4 GEMMs per layer) leg")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (the known-size "
@@ -250,6 +253,37 @@ def main() -> int:
 
     if args.sweep:
         sweep(mats, dev, max(5, args.steps // 5), 3)
+
+    if not args.no_merged:
+        # Same weight bytes with q/k/v and gate/up merged (4 GEMMs per layer),
+        # as the reference's Marlin loader runs a decoder stage.
+        from gptq_synth import LLAMA2_7B_MERGED_SHAPES
+        del _cache
+        mats.clear()
+        torch.cuda.empty_cache()
+        mmats, _mcache = build_matrices(dev, args.layers, max(args.prefill_m, 1),
+                                        shapes=LLAMA2_7B_MERGED_SHAPES)
+        mms, _, _ = time_graph(mmats, 1, args.steps, args.warmup, dev)
+        mbytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mmats)
+        mg = mbytes / (mms * 1e-3) / 1e9
+        log(f"merged decode M=1: {mms * 1e3:.1f} us per step ({len(mmats)} GEMMs), {mg:.1f} GB/s")
+        merged = {"value": round(mg, 2), "unit": "GB/s", "ms_per_step": round(mms, 5),
+                  "launches_per_step": len(mmats), "frac": round(mg / HBM_PEAK_GBS, 4),
+                  "workload": "same 8 layers with q/k/v merged (4096x12288) and gate/up merged "
+                              "(4096x22016): 4 GEMMs per layer"}
+        if not args.no_prefill:
+            m = args.prefill_m
+            pms, _, _ = time_graph(mmats, m, max(5, args.steps // 5), max(2, args.warmup // 5), dev)
+            tf = sum(flops(m, k, n) for _, k, n, _ in mmats) / (pms * 1e-3) / 1e12
+            log(f"merged prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
+            merged["prefill"] = {"m": m, "value": round(tf, 2), "unit": "TFLOP/s",
+                                 "ms_per_step": round(pms, 5),
+                                 "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+        result["merged"] = merged
+        if args.sweep:
+            sweep(mmats, dev, max(5, args.steps // 5), 3,
+                  shapes=((4096, 12288), (4096, 22016)))
+        del mmats, _mcache
 
     if not args.no_cpu:
         log("timing CPU baseline")

@@ -109,6 +109,13 @@ LLAMA2_7B_SHAPES = {
     "o_proj": (4096, 4096), "gate_proj": (4096, 11008), "up_proj": (4096, 11008),
     "down_proj": (11008, 4096),
 }
+# The same layer with q/k/v and gate/up merged along the output dimension,
+# the decode topology of the reference's Marlin loader
+# (operators/assemble/decoders/real_loader_marlin.py:61-79).
+LLAMA2_7B_MERGED_SHAPES = {
+    "qkv_proj": (4096, 12288), "o_proj": (4096, 4096), "gate_up_proj": (4096, 22016),
+    "down_proj": (11008, 4096),
+}
 LLAMA2_13B_SHAPES = {
     "q_proj": (5120, 5120), "k_proj": (5120, 5120), "v_proj": (5120, 5120),
     "o_proj": (5120, 5120), "gate_proj": (5120, 13824), "up_proj": (5120, 13824),

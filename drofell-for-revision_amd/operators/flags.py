@@ -4,8 +4,8 @@ Same names and meaning as the reference's ``operators/flags.py:8-10``
 (paths relative to ``/root/reference/After-Revision-DROFELL``).
 """
 
-# Keep a dequantised fp16 copy of every weight after post_init (forward
-# then still runs the packed kernels; the copy serves the backward).
+# Keep a dequantised fp16 copy of every weight after post_init; the forward
+# then takes the dense route over that copy, as in the reference.
 RECONSTRUCTE_WEIGTH_FLOAT16 = False
 # bf16 reconstruction is not offered by the HIP backend (fp16 only).
 RECONSTRUCTE_WEIGTH_BFLOAT16 = False
