@@ -51,19 +51,17 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n);
 // split count: with too little workspace the call runs unsplit.
 dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_bytes, bool cap_by_ws) {
   dw4::PrefillPlan p;
-  p.bm = m < DW4_PREFILL_BM128_MIN_M ? 64 : 128;
+  // Row tile: 16 or 32 rows just covering small M, then 64 or 128.  Fewer
+  // rows per tile mean fewer MFMA uses per dequantised weight fragment, so
+  // the small tiles are only for small M.
+  p.bm = m <= 16 ? 16 : m <= 32 ? 32 : m < dw4::kPrefillBm128MinM ? 64 : 128;
   p.bn = n >= 2048 ? 256 : 128;
-  p.occ = (p.bm == 64 && p.bn == 256) ? DW4_PREFILL_OCC : 1;
-  if (DW4_PREFILL_NARROW128 && p.bm == 128) {  // 128x128 tiles, two workgroups per CU
-    p.bn = 128;
-    p.occ = 2;
-  }
   const int kc = k / kChunkK;
   const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
   int splits = split_req;
   if (splits <= 0) {
-    const int slots = cu_count() * p.occ;  // workgroups resident at once
-    splits = tiles >= slots ? 1 : slots / tiles;
+    const int cus = cu_count();  // one workgroup per CU at a time
+    splits = tiles >= cus ? 1 : cus / tiles;
     splits = std::min(splits, std::max(1, kc / 4));
     splits = std::min(splits, 16);
   }

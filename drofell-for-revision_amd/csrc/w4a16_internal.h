@@ -17,18 +17,6 @@ constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 #ifndef DW4_DECODE_UMAX
 #define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
 #endif
-#ifndef DW4_PREFILL_PB
-#define DW4_PREFILL_PB 4  // prefill weight ring depth (chunks) of the 64x256 tile
-#endif
-#ifndef DW4_PREFILL_BM128_MIN_M
-#define DW4_PREFILL_BM128_MIN_M 513  // smallest M that gets 128-row prefill tiles
-#endif
-#ifndef DW4_PREFILL_NARROW128
-#define DW4_PREFILL_NARROW128 0  // 128-row tiles use 128 columns and two workgroups per CU
-#endif
-#ifndef DW4_PREFILL_OCC
-#define DW4_PREFILL_OCC 1  // workgroups per CU of the 64x256 prefill tile
-#endif
 #ifndef DW4_DECODE_NARROW_WAVES
 #define DW4_DECODE_NARROW_WAVES 16  // waves per workgroup when strips <= CUs and M <= 4
 #endif
@@ -49,10 +37,12 @@ struct GemmArgs {
   int64_t ldy;
 };
 
+// Prefill launch: row tile bm (16: 16x16x32 MFMA kernel; 32, 64, 128:
+// 32x32x16 MFMA kernel), column tile bn (128 or 256), split-K factor.
 struct PrefillPlan {
   int bm, bn, splits;
-  int occ = 1;  // workgroups per CU the kernel variant is built for (1 or 2)
 };
+constexpr int kPrefillBm128MinM = 513;  // smallest M that gets 128-row prefill tiles
 
 struct DecodePlan {
   int splits;   // workgroups along K per strip

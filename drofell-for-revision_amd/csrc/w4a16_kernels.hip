@@ -170,8 +170,8 @@ __device__ __forceinline__ h8 load_x_unit(const _Float16* __restrict__ row,
 // fp16); the scale is applied per group in fp32; the waves' partial sums
 // meet in LDS in a fixed order at the end (deterministic).
 // ---------------------------------------------------------------------------
-constexpr int kXBatch = 4;  // activation units per lane in the first staging pass
-constexpr int kMBatch = 4;  // metadata dwords per lane in the first staging pass
+constexpr int kXBatch = 8;  // activation units per lane per staging batch
+constexpr int kMBatch = 4;  // metadata dwords per lane per staging batch
 constexpr int kLdx = kChunkK + 8;  // halfs per staged activation row (16-byte pad)
 
 template <int MT, int WAVES, int U, bool G128, bool ACT>
@@ -253,8 +253,25 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 #pragma unroll
   for (int b = 0; b < kMBatch; ++b)
     if (lane + 64 * b < munits) mw[lane + 64 * b] = mv[b];
-  for (int u = lane + 64 * kXBatch; u < xunits; u += 64) *(h8*)x_dst(u) = x_unit(u);
-  for (int v = lane + 64 * kMBatch; v < munits; v += 64) mw[v] = m_word(v);
+  // The rest (M > 1 or many chunks) in batches: all loads of a batch are in
+  // flight before its first store, so the staging costs one L2 round trip
+  // per batch rather than one per 16-byte unit.
+  for (int u0 = lane + 64 * kXBatch; u0 < xunits; u0 += 64 * kXBatch) {
+#pragma unroll
+    for (int b = 0; b < kXBatch; ++b)
+      if (u0 + 64 * b < xunits) xv[b] = x_unit(u0 + 64 * b);
+#pragma unroll
+    for (int b = 0; b < kXBatch; ++b)
+      if (u0 + 64 * b < xunits) *(h8*)x_dst(u0 + 64 * b) = xv[b];
+  }
+  for (int v0 = lane + 64 * kMBatch; v0 < munits; v0 += 64 * kMBatch) {
+#pragma unroll
+    for (int b = 0; b < kMBatch; ++b)
+      if (v0 + 64 * b < munits) mv[b] = m_word(v0 + 64 * b);
+#pragma unroll
+    for (int b = 0; b < kMBatch; ++b)
+      if (v0 + 64 * b < munits) mw[v0 + 64 * b] = mv[b];
+  }
   // The wave reads back only what it wrote; LDS operations of one wave
   // complete in order, so no workgroup barrier is needed here.
 
@@ -377,7 +394,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 }
 
 // ---------------------------------------------------------------------------
-// Prefill kernel (any M): 4 waves; workgroup tile (16*MT2) rows x (64*S)
+// Prefill kernel, 16x16x32 MFMA form (used for 16-row tiles; larger tiles
+// use prefill32_kernel below): 4 waves; workgroup tile (16*MT2) rows x (64*S)
 // columns; waves split the columns (S strips each) and share the rows.
 // Activations (L2-resident) are staged per 128-row chunk into double-
 // buffered LDS one chunk ahead (gathered through perm for act-order).  Each
@@ -392,8 +410,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 constexpr int kLdaPad = 8;
 constexpr int kLda = kChunkK + kLdaPad;  // halfs per LDS row (272 bytes)
 
-template <int MT2, int S, int PB, int GPC, bool ACT, int OCC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
+template <int MT2, int S, int PB, int GPC, bool ACT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                const int32_t* __restrict__ perm,
                const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
@@ -488,16 +506,11 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     for (int si = 0; si < S; ++si) acc[mt][si] = f4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t magic = kMagic;
-  // OCC == 1 (one workgroup per CU, one wave per SIMD): a wave has to hide
-  // its own latencies, so the four 32-row k-steps of a chunk are software
-  // pipelined -- while the MFMAs of step t run, the wave reads the A
-  // fragments of step t+1 from LDS and dequantises the B fragments of step
-  // t+1 (independent VALU work the scheduler interleaves with the MFMAs) --
-  // and activations are fetched two chunks ahead.
-  // OCC == 2 (two workgroups per CU, 256 registers per wave): the other
-  // wave on the SIMD overlaps its VALU and MFMA work with this one's, so the
-  // registers go to a plain schedule and a one-chunk activation prefetch.
-  constexpr bool PIPE = OCC == 1;
+  // One workgroup per CU, one wave per SIMD: a wave has to hide its own
+  // latencies, so the four 32-row k-steps of a chunk are software pipelined
+  // -- while the MFMAs of step t run, the wave reads the A fragments of step
+  // t+1 from LDS and dequantises the B fragments of step t+1 -- and
+  // activations are fetched two chunks ahead.
   auto dequant = [&](int slot_u, int t, h8 (&bop)[S]) {
     const int gl = GPC == 1 ? 0 : (t * GPC) / 4;
 #pragma unroll
@@ -512,53 +525,38 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   };
   auto compute = [&](int slot_u, int buf) {
     const _Float16* Ab = &As[buf][(size_t)j * kLda + 8 * kq];
-    if constexpr (PIPE) {
-      h8 af[2][MT2];
-      h8 bop[2][S];
+    h8 af[2][MT2];
+    h8 bop[2][S];
 #pragma unroll
-      for (int mt = 0; mt < MT2; ++mt) af[0][mt] = *(const h8*)(Ab + mt * 16 * kLda);
-      dequant(slot_u, 0, bop[0]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int mt = 0; mt < MT2; ++mt) af[0][mt] = *(const h8*)(Ab + mt * 16 * kLda);
+    dequant(slot_u, 0, bop[0]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t < 3) {
-#pragma unroll
-          for (int mt = 0; mt < MT2; ++mt)
-            af[(t + 1) & 1][mt] = *(const h8*)(Ab + mt * 16 * kLda + 32 * (t + 1));
-          dequant(slot_u, t + 1, bop[(t + 1) & 1]);
-        }
+    for (int t = 0; t < 4; ++t) {
+      if (t < 3) {
 #pragma unroll
         for (int mt = 0; mt < MT2; ++mt)
-#pragma unroll
-          for (int si = 0; si < S; ++si)
-            acc[mt][si] = mfma16(af[t & 1][mt], bop[t & 1][si], acc[mt][si]);
-        __builtin_amdgcn_sched_barrier(0);
+          af[(t + 1) & 1][mt] = *(const h8*)(Ab + mt * 16 * kLda + 32 * (t + 1));
+        dequant(slot_u, t + 1, bop[(t + 1) & 1]);
       }
-    } else {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        h8 bop[S];
-        dequant(slot_u, t, bop);
+      for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < MT2; ++mt) {
-          const h8 af = *(const h8*)(Ab + mt * 16 * kLda + 32 * t);
-#pragma unroll
-          for (int si = 0; si < S; ++si) acc[mt][si] = mfma16(af, bop[si], acc[mt][si]);
-        }
-      }
+        for (int si = 0; si < S; ++si)
+          acc[mt][si] = mfma16(af[t & 1][mt], bop[t & 1][si], acc[mt][si]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Activations travel global -> registers AD chunks ahead of their use and
-  // registers -> LDS one step ahead, so with AD == 2 a step only waits for
-  // loads issued a whole step earlier.  areg[i % AD] holds chunk i+AD while
-  // chunk i is computed (PB is even, so the parity is a compile-time index).
+  // Activations travel global -> registers two chunks ahead of their use and
+  // registers -> LDS one step ahead, so a step only waits for loads issued a
+  // whole step earlier.  areg[i & 1] holds chunk i+2 while chunk i is
+  // computed (PB is even, so the parity is a compile-time index).
   static_assert(PB % 2 == 0, "ring depth must be even");
-  constexpr int AD = PIPE ? 2 : 1;
-  h8 areg[AD][UNITS];
+  h8 areg[2][UNITS];
   // prologue: ring filled with the first PB chunks (only those that exist
-  // when the split is shorter than the ring), chunk 0 in LDS, chunks
-  // 1..AD-1 in registers
+  // when the split is shorter than the ring), chunk 0 in LDS, chunk 1 in
+  // registers
 #pragma unroll
   for (int u = 0; u < PB; ++u)
     if (u < nchunks) load_b(u, u);
@@ -566,19 +564,17 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     load_a(c_begin, areg[0]);
     store_a(0, areg[0]);
   }
-  if (AD == 2 && nchunks > 1) load_a(c_begin + 1, areg[AD - 1]);
+  if (nchunks > 1) load_a(c_begin + 1, areg[1]);
   __syncthreads();
 
-  // One step: fetch chunk i+AD's activations, compute chunk i from slot u,
+  // One step: fetch chunk i+2's activations, compute chunk i from slot u,
   // refill slot u with chunk i + PB, publish chunk i+1's activations.
   auto step = [&](int u, int i, bool refill) {
     const int p = u & 1;  // == i & 1
-    const int ra = AD == 2 ? p : 0;
-    const int rs = AD == 2 ? p ^ 1 : 0;
-    if (i + AD < nchunks) load_a(c_begin + i + AD, areg[ra]);
+    if (i + 2 < nchunks) load_a(c_begin + i + 2, areg[p]);
     compute(u, p);
     if (refill) load_b(u, i + PB);
-    if (i + 1 < nchunks) store_a(p ^ 1, areg[rs]);
+    if (i + 1 < nchunks) store_a(p ^ 1, areg[p ^ 1]);
     __syncthreads();
   };
   int i0 = 0;
@@ -711,6 +707,327 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       for (int si = 0; si < S; ++si) sum[mt][si] += t[mt][si];
   }
   write_tile([&](int mt, int si, int r) { return sum[mt][si][r]; });
+  if (tid == 0) __hip_atomic_store(&counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill kernel, 32x32x16 MFMA form (the default for M > 32).  Same
+// workgroup tile, activation staging, weight ring and split-K protocol as
+// prefill_kernel; each wave covers 32*MT3 rows x 32*P columns with
+// v_mfma_f32_32x32x16_f16.  One wave alone issues that instruction at ~94%
+// of the MFMA peak, where it issues the 16x16x32 form at ~55%, so the
+// kernel no longer needs a second wave per SIMD to keep the matrix core fed.
+//
+// The packed layout stays the 16x16x32 one: word w of lane l of a strip
+// holds rows 32w + 8(l/16) .. +7 of column l%16.  The 32x32x16 B operand of
+// k-step t needs, in lane L, rows 16t + 8(L/32) .. +7 of column L%32 of a
+// strip pair.  For two strips' word w (A in the first strip, B in the
+// second, 16-lane rows A0..A3, B0..B3) that is [A0 B0 A1 B1] for t = 2w and
+// [A2 B2 A3 B3] for t = 2w + 1: one v_permlane16_swap ([A0 B0 A2 B2],
+// [A1 B1 A3 B3]) followed by one v_permlane32_swap.
+// Accumulator element i of lane L is row 8(i/4) + 4(L/32) + i%4, column
+// L%32 of the 32x32 tile.
+// ---------------------------------------------------------------------------
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void strip_pair_to_b32(uint32_t a, uint32_t b, uint32_t& even,
+                                                  uint32_t& odd) {
+  const auto x = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  const auto y = __builtin_amdgcn_permlane32_swap(x[0], x[1], false, false);
+  even = y[0];
+  odd = y[1];
+}
+
+template <int MT3, int P, int PB, int GPC, bool ACT>
+__global__ void __launch_bounds__(256)
+prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
+                 const int32_t* __restrict__ perm,
+                 const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
+                 const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
+                 uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
+                 int* __restrict__ counters, int K, int N, int gs, int G, int chunks_per_split,
+                 int mtiles, int ntiles) {
+  constexpr int S = 2 * P;               // 16-column strips per wave
+  constexpr int BM = 32 * MT3;
+  constexpr int UNITS = BM * 16 / 256;   // 16-byte activation units per thread per chunk
+  constexpr int NSLOT = MT3 * P * 16;    // accumulator floats per lane
+  static_assert(PB % 2 == 0, "ring depth must be even");
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * kLda];
+
+  // XCD-aware tile order (as prefill_kernel)
+  const int b = blockIdx.x;
+  const int q8 = b / (8 * mtiles);
+  const int r8 = b % (8 * mtiles);
+  const int mtile = r8 / 8;
+  const int ntile = q8 * 8 + (r8 % 8);
+  if (ntile >= ntiles) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hb = lane >> 5;         // k half of the 32x32x16 operands
+  const int hi = (lane >> 4) & 1;   // which strip of a pair this lane's B column is in
+  const int j = lane & 15;
+  const int KC = K / kChunkK;
+  const int split = blockIdx.y;
+  const int c_begin = split * chunks_per_split;
+  const int nchunks = min(KC, c_begin + chunks_per_split) - c_begin;
+  const int m0 = mtile * BM;
+  const int NS = N / kStripN;
+
+  const _Float16* arow[UNITS];
+  int aoff[UNITS];
+#pragma unroll
+  for (int i = 0; i < UNITS; ++i) {
+    const int u = tid + 256 * i;
+    arow[i] = x + (size_t)min(m0 + (u >> 4), M - 1) * ldx;
+    aoff[i] = (u >> 4) * kLda + (u & 15) * 8;
+  }
+  auto load_a = [&](int c, h8 (&regs)[UNITS]) {
+#pragma unroll
+    for (int i = 0; i < UNITS; ++i)
+      regs[i] = load_x_unit<ACT>(arow[i], perm, c * kChunkK + ((tid + 256 * i) & 15) * 8);
+  };
+  auto store_a = [&](int buf, const h8 (&regs)[UNITS]) {
+#pragma unroll
+    for (int i = 0; i < UNITS; ++i) *(h8*)(&As[buf][aoff[i]]) = regs[i];
+  };
+
+  // packed words: strips strip0 .. strip0+S-1 (the last N-tile may be partial)
+  const int strip0 = ntile * 4 * S + wave * S;
+  const u4* qp[S];
+#pragma unroll
+  for (int si = 0; si < S; ++si) {
+    const int st = strip0 + si;
+    qp[si] = pq + ((size_t)(st < NS ? st : 0) * KC + c_begin) * 64 + lane;
+  }
+  // scale / zero words of this lane's B column in each strip pair
+  const uint32_t* sp[P];
+  const uint32_t* zp[P];
+  bool pval[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int st = strip0 + 2 * p + hi;
+    pval[p] = st < NS;
+    const int sc = pval[p] ? st : 0;
+    sp[p] = ps32 + (size_t)sc * G * 8 + (j >> 1);
+    zp[p] = pz + (size_t)sc * G * 2 + (j >> 3);
+  }
+  const int hsh = (j & 1) * 16;
+  const int zsh = (j & 7) * 4;
+
+  u4 qb[PB][S];
+  uint32_t sb[PB][P][GPC], zb[PB][P][GPC];
+  auto load_b = [&](int slot_u, int i) {
+    const int c = c_begin + i;
+#pragma unroll
+    for (int si = 0; si < S; ++si) qb[slot_u][si] = __builtin_nontemporal_load(qp[si] + (size_t)i * 64);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int gl = 0; gl < GPC; ++gl) {
+        const int g = GPC == 1 ? (c * kChunkK) / gs : c * GPC + gl;
+        sb[slot_u][p][gl] = sp[p][(size_t)g * 8];
+        zb[slot_u][p][gl] = zp[p][(size_t)g * 2];
+      }
+  };
+
+  f16v acc[MT3][P];
+#pragma unroll
+  for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[mt][p][e] = 0.f;
+
+  const uint32_t magic = kMagic;
+  // Software pipeline over the 8 k-steps of a chunk: the region of step t
+  // holds the MFMAs of step t (operands dequantised in the previous region)
+  // and the dequantisation and A-fragment reads of step t+1, independent
+  // work the scheduler can interleave.  (Measured on gfx950: a wave's dequant
+  // VALU and its own 32x32x16 MFMAs hardly overlap, whatever the order, so
+  // the cost per chunk is close to their sum; the VALU per MFMA is what
+  // bounds this kernel.)
+  auto dequant_step = [&](int slot_u, int t, h8 (&bop)[P]) {
+    const int w = t >> 1;
+    const int gl = GPC == 1 ? 0 : (t * GPC) / 8;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      uint32_t ev, od;
+      strip_pair_to_b32(qb[slot_u][2 * p][w], qb[slot_u][2 * p + 1][w], ev, od);
+      h2 nz1024, nz64;
+      zero_consts(zb[slot_u][p][gl], zsh, nz1024, nz64);
+      const _Float16 sc = as_h((uint16_t)(sb[slot_u][p][gl] >> hsh));
+      const h8 d = centered8((t & 1) ? od : ev, nz1024, nz64, magic);
+      const h8 s8 = h8{sc, sc, sc, sc, sc, sc, sc, sc};
+      bop[p] = d * s8;  // fp16 product, round to nearest even
+    }
+  };
+  auto compute = [&](int slot_u, int buf) {
+    const _Float16* Ab = &As[buf][(size_t)l32 * kLda + 8 * hb];
+    h8 bop[2][P];
+    h8 af[2][MT3];
+    dequant_step(slot_u, 0, bop[0]);
+#pragma unroll
+    for (int mt = 0; mt < MT3; ++mt) af[0][mt] = *(const h8*)(Ab + mt * 32 * kLda);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int cur = t & 1;
+      if (t < 7) {
+#pragma unroll
+        for (int mt = 0; mt < MT3; ++mt)
+          af[cur ^ 1][mt] = *(const h8*)(Ab + mt * 32 * kLda + 16 * (t + 1));
+        dequant_step(slot_u, t + 1, bop[cur ^ 1]);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc[mt][p] = mfma32(af[cur][mt], bop[cur][p], acc[mt][p]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // activations two chunks ahead in registers, one step ahead in LDS
+  h8 areg[2][UNITS];
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (u < nchunks) load_b(u, u);
+  if (nchunks > 0) {
+    load_a(c_begin, areg[0]);
+    store_a(0, areg[0]);
+  }
+  if (nchunks > 1) load_a(c_begin + 1, areg[1]);
+  __syncthreads();
+  auto step = [&](int u, int i, bool refill) {
+    const int pp = u & 1;  // == i & 1
+    if (i + 2 < nchunks) load_a(c_begin + i + 2, areg[pp]);
+    compute(u, pp);
+    if (refill) load_b(u, i + PB);
+    if (i + 1 < nchunks) store_a(pp ^ 1, areg[pp ^ 1]);
+    __syncthreads();
+  };
+  int i0 = 0;
+  for (; i0 + 2 * PB <= nchunks; i0 += PB) {
+#pragma unroll
+    for (int u = 0; u < PB; ++u) step(u, i0 + u, true);
+  }
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (i0 + u < nchunks) step(u, i0 + u, i0 + u + PB < nchunks);
+#pragma unroll
+  for (int u = 0; u < PB; ++u)
+    if (i0 + PB + u < nchunks) step(u, i0 + PB + u, false);
+
+  // Output through LDS in row order, 16-byte row segments (see prefill_kernel)
+  constexpr int TW = 32 * P;
+  constexpr int SEG = TW / 8;
+  constexpr int RPP = 64 / SEG;
+  static_assert(4 * BM * TW <= 2 * BM * kLda, "output tiles fit in the activation buffers");
+  _Float16 bv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int st = strip0 + 2 * p + hi;
+    bv[p] = (bias != nullptr && st < NS) ? as_h(bias[st * kStripN + j]) : (_Float16)0.f;
+  }
+  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0);
+  auto write_tile = [&](auto&& val) {  // val(mt, p, i): fp32 result of that accumulator slot
+    _Float16* T = &As[0][0] + wave * (BM * TW);
+#pragma unroll
+    for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          _Float16 out = (_Float16)val(mt, p, i);
+          if (bias != nullptr) out = out + bv[p];
+          T[(mt * 32 + 8 * (i >> 2) + 4 * hb + (i & 3)) * TW + p * 32 + l32] = out;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int pass = 0; pass < BM / RPP; ++pass) {
+      const int row = pass * RPP + lane / SEG;
+      const int seg = lane % SEG;
+      const int m = m0 + row;
+      const int strip = strip0 + seg / 2;
+      if (m < M && strip < NS) {
+        const u4 v = *(const u4*)&T[row * TW + seg * 8];
+        uint16_t* dst = y + (size_t)m * ldy + strip * kStripN + (seg & 1) * 8;
+        if (vec_y) {
+          *(u4*)dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dst[2 * e] = (uint16_t)(v[e] & 0xFFFFu);
+            dst[2 * e + 1] = (uint16_t)(v[e] >> 16);
+          }
+        }
+      }
+    }
+  };
+  const int splits = gridDim.y;
+  if (splits == 1) {
+    write_tile([&](int mt, int p, int i) { return acc[mt][p][i]; });
+    return;
+  }
+
+  // Split-K: write-through partials, last arriver sums in split order (as
+  // prefill_kernel).  Layout per split plane: [tile][slot][256 threads],
+  // slot = (mt * P + p) * 16 + i.
+  const int tile_id = mtile * ntiles + ntile;
+  const size_t plane = (size_t)mtiles * ntiles * NSLOT * 256;
+  const size_t tbase = (size_t)tile_id * NSLOT * 256 + tid;
+#pragma unroll
+  for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __hip_atomic_store(&part[(size_t)split * plane + tbase + ((mt * P + p) * 16 + i) * 256],
+                           acc[mt][p][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ int last_arrival;
+  __syncthreads();
+  if (tid == 0) {
+    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELEASE,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == splits - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last_arrival = last;
+  }
+  __syncthreads();
+  if (!last_arrival) return;
+  f16v sum[MT3][P];
+#pragma unroll
+  for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum[mt][p][i] = 0.f;
+  for (int sp2 = 0; sp2 < splits; ++sp2) {
+    if (sp2 == split) {
+#pragma unroll
+      for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+        for (int p = 0; p < P; ++p) sum[mt][p] += acc[mt][p];
+      continue;
+    }
+    const float* src = part + (size_t)sp2 * plane + tbase;
+#pragma unroll
+    for (int mt = 0; mt < MT3; ++mt)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        f16v t;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t[i] = src[((mt * P + p) * 16 + i) * 256];
+        sum[mt][p] += t;
+      }
+  }
+  write_tile([&](int mt, int p, int i) { return sum[mt][p][i]; });
   if (tid == 0) __hip_atomic_store(&counters[tile_id], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -860,7 +1177,7 @@ hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hi
   }
 }
 
-template <int MT2, int S, int PB, int GPC, bool ACT, int OCC>
+template <int MT2, int S, int PB, int GPC, bool ACT>
 static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
   constexpr int BM = 16 * MT2;
   constexpr int BN = 64 * S;
@@ -875,19 +1192,53 @@ static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, void* ws, hi
                     ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
                     : nullptr;
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
-  prefill_kernel<MT2, S, PB, GPC, ACT, OCC><<<grid, 256, 0, stream>>>(
+  prefill_kernel<MT2, S, PB, GPC, ACT><<<grid, 256, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
       a.bias, a.y, a.ldy, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   return hipGetLastError();
 }
 
-template <int MT2, int S, int PB, int OCC>
+template <int MT3, int P, int PB, int GPC, bool ACT>
+static hipError_t launch_prefill32_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
+  constexpr int BM = 32 * MT3;
+  constexpr int BN = 128 * P;
+  const int mtiles = (a.M + BM - 1) / BM;
+  const int ntiles = (a.N + BN - 1) / BN;
+  const int KC = a.K / kChunkK;
+  const int cps = (KC + splits - 1) / splits;
+  const int real_splits = (KC + cps - 1) / cps;
+  if (real_splits > 1 && mtiles * ntiles > kSplitCounters) return hipErrorInvalidValue;
+  int* counters = static_cast<int*>(ws);
+  float* part = real_splits > 1
+                    ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
+                    : nullptr;
+  const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
+  prefill32_kernel<MT3, P, PB, GPC, ACT><<<grid, 256, 0, stream>>>(
+      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
+      a.bias, a.y, a.ldy, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
+  return hipGetLastError();
+}
+
+template <int MT3, int P, int PB>
+static hipError_t launch_prefill32_tile(const GemmArgs& a, int splits, void* part, hipStream_t stream) {
+  const bool act = a.perm != nullptr;
+  const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
+#define DW4_PREFILL32_G(GG)                                                            \
+  return act ? launch_prefill32_cfg<MT3, P, PB, GG, true>(a, splits, part, stream)    \
+             : launch_prefill32_cfg<MT3, P, PB, GG, false>(a, splits, part, stream)
+  if (gpc == 1) { DW4_PREFILL32_G(1); }
+  if (gpc == 2) { DW4_PREFILL32_G(2); }
+  DW4_PREFILL32_G(4);
+#undef DW4_PREFILL32_G
+}
+
+template <int MT2, int S, int PB>
 static hipError_t launch_prefill_tile(const GemmArgs& a, int splits, void* part, hipStream_t stream) {
   const bool act = a.perm != nullptr;
   const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
-#define DW4_PREFILL_G(GG)                                                               \
-  return act ? launch_prefill_cfg<MT2, S, PB, GG, true, OCC>(a, splits, part, stream)    \
-             : launch_prefill_cfg<MT2, S, PB, GG, false, OCC>(a, splits, part, stream)
+#define DW4_PREFILL_G(GG)                                                          \
+  return act ? launch_prefill_cfg<MT2, S, PB, GG, true>(a, splits, part, stream)    \
+             : launch_prefill_cfg<MT2, S, PB, GG, false>(a, splits, part, stream)
   if (gpc == 1) { DW4_PREFILL_G(1); }
   if (gpc == 2) { DW4_PREFILL_G(2); }
   DW4_PREFILL_G(4);
@@ -895,19 +1246,17 @@ static hipError_t launch_prefill_tile(const GemmArgs& a, int splits, void* part,
 }
 
 hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* part, hipStream_t stream) {
-  // Four strips per wave (BN = 256) give each LDS activation read four MFMA
-  // uses; measured LDS bandwidth (~128 B/clk/CU) makes two strips per wave
-  // LDS-bound.  The register ring is shallower for the wider tiles.
-  if (plan.bm == 64 && plan.bn == 256) {
-    if (plan.occ == 2) return launch_prefill_tile<4, 4, 2, 2>(a, plan.splits, part, stream);
-    return launch_prefill_tile<4, 4, DW4_PREFILL_PB, 1>(a, plan.splits, part, stream);
-  }
-  if (plan.bm == 128 && plan.bn == 256) return launch_prefill_tile<8, 4, 2, 1>(a, plan.splits, part, stream);
-  if (plan.bm == 64 && plan.bn == 128) return launch_prefill_tile<4, 2, 4, 1>(a, plan.splits, part, stream);
-  if (plan.bm == 128 && plan.bn == 128) {
-    if (plan.occ == 2) return launch_prefill_tile<8, 2, 2, 2>(a, plan.splits, part, stream);
-    return launch_prefill_tile<8, 2, 4, 1>(a, plan.splits, part, stream);
-  }
+  // Waves split the columns: 64 (bn = 256) or 32 (bn = 128) per wave.  Four
+  // 16-column strips per wave give each LDS activation read four MFMA uses;
+  // measured LDS bandwidth (~128 B/clk/CU) makes fewer LDS-bound.
+  if (plan.bm == 16 && plan.bn == 256) return launch_prefill_tile<1, 4, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 16 && plan.bn == 128) return launch_prefill_tile<1, 2, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 32 && plan.bn == 256) return launch_prefill32_tile<1, 2, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 32 && plan.bn == 128) return launch_prefill32_tile<1, 1, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 64 && plan.bn == 256) return launch_prefill32_tile<2, 2, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 64 && plan.bn == 128) return launch_prefill32_tile<2, 1, 4>(a, plan.splits, part, stream);
+  if (plan.bm == 128 && plan.bn == 256) return launch_prefill32_tile<4, 2, 2>(a, plan.splits, part, stream);
+  if (plan.bm == 128 && plan.bn == 128) return launch_prefill32_tile<4, 1, 4>(a, plan.splits, part, stream);
   return hipErrorInvalidValue;
 }
 
