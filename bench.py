@@ -162,6 +162,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-merged", action="store_true",
                     help="skip the merged-projection (4 GEMMs per layer) leg")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="run only the M=--prefill-m leg (for hardware-counter passes)")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (the known-size "
@@ -192,6 +194,12 @@ def main() -> int:
                        for _, _, _, q4 in mats)
 
     torch.cuda.synchronize(dev)
+    if args.only_prefill:
+        m = args.prefill_m
+        pms, _, _ = time_graph(mats, m, args.steps, args.warmup, dev)
+        tf = sum(flops(m, k, n) for _, k, n, _ in mats) / (pms * 1e-3) / 1e12
+        log(f"prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
+        return 0
     ms, wall, _ = time_graph(mats, 1, args.steps, args.warmup, dev)
     step_bytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
     gbs = step_bytes / (ms * 1e-3) / 1e9
