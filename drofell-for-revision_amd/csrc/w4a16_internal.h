@@ -17,6 +17,9 @@ constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 #ifndef DW4_DECODE_UMAX
 #define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
 #endif
+#ifndef DW4_DECODE_REG_MIN_M
+#define DW4_DECODE_REG_MIN_M 5  // smallest M for the register-fed decode kernel
+#endif
 #ifndef DW4_DECODE_NARROW_WAVES
 #define DW4_DECODE_NARROW_WAVES 16  // waves per workgroup when strips <= CUs and M <= 4
 #endif
@@ -47,9 +50,12 @@ constexpr int kPrefillBm128MinM = 513;  // smallest M that gets 128-row prefill 
 struct DecodePlan {
   int splits;   // workgroups along K per strip
   int cps;      // 128-row chunks per split
-  int waves;    // waves per workgroup (4 or 8)
+  int waves;    // waves per workgroup (4, 8 or 16)
   size_t smem;  // dynamic LDS bytes per workgroup
+  bool reg = false;  // register-fed kernel (activations not staged in LDS)
+  int ss = 1;        // strips per workgroup of the register-fed kernel
 };
+constexpr int kDecodeRegMinM = DW4_DECODE_REG_MIN_M;
 
 // LDS bytes a decode workgroup needs for a K range of `cps` chunks: each of
 // its waves stages the activation rows and metadata records of its own
@@ -72,6 +78,17 @@ inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
 inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus) {
   const int kc = k / kChunkK;
   const int strips = n / kStripN;
+  if (m >= kDecodeRegMinM && m <= 16) {
+    // register-fed: never split; two strips per workgroup share the A
+    // fragments when that still leaves a workgroup per CU; 16 waves when
+    // there are no more workgroups than CUs
+    DecodePlan r{1, kc, 8, 0};
+    r.reg = true;
+    r.ss = (strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
+    if ((strips + r.ss - 1) / r.ss <= cus && kc >= 32) r.waves = 16;
+    r.smem = (size_t)r.waves * r.ss * 64 * 16;
+    return r;
+  }
   int waves = 8;
   if (strips >= 2 * cus && m <= 16) waves = 4;
   else if (strips <= cus && m <= 4) waves = kDecodeNarrowWaves;
@@ -96,6 +113,7 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
                          const int32_t* perm, uint32_t* pq, uint32_t* pz, uint16_t* ps,
                          int K, int N, int G, hipStream_t stream);
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream);
+hipError_t launch_decode_reg(const GemmArgs& a, const DecodePlan& p, hipStream_t stream);
 // Workspace of a split-K call: a fixed head of kSplitCounters int32 arrival
 // counters (one per prefill output tile; zero before the first call and left
 // zero by every call), then one fp32 partial plane per split: [M][N] for the

@@ -394,6 +394,177 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 }
 
 // ---------------------------------------------------------------------------
+// Decode kernel, register-fed form (5 <= M <= 16).  The staged kernel above
+// copies each strip's whole activation block into LDS before it starts; at
+// M = 16 that block (M * K * 2 bytes per strip) exceeds what three
+// workgroups per CU can hold, so the staged kernel splits K and runs in
+// several rounds.  Here each wave loads its A fragments (16 bytes per lane
+// per 32-row k-step, from L2) into the same register ring as the weights,
+// and SS adjacent strips share them, so no LDS is needed until the final
+// cross-wave reduction and K is never split.
+// ---------------------------------------------------------------------------
+template <int WAVES, int U, int SS, int GPC, bool ACT>
+__global__ void __launch_bounds__(WAVES * 64)
+decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
+                  const int32_t* __restrict__ perm,
+                  const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
+                  const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
+                  uint16_t* __restrict__ y, int64_t ldy, int K, int N, int gs, int G) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int T = WAVES * 64;
+  constexpr int SPG = 4 / GPC;  // 32-row k-steps per group
+  const int s0 = blockIdx.x * SS;
+  const int NS = N / kStripN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15;
+  const int kq = lane >> 4;
+  const int KC = K / kChunkK;
+  const int nch = wave < KC ? (KC - wave + WAVES - 1) / WAVES : 0;
+  // A rows: lanes past the last row read row M-1 (never stored)
+  const _Float16* xr = x + (size_t)min(j, M - 1) * ldx;
+
+  const u4* qp[SS];
+  const uint32_t* sp[SS];
+  const uint32_t* zp[SS];
+#pragma unroll
+  for (int ss = 0; ss < SS; ++ss) {
+    const int st = min(s0 + ss, NS - 1);
+    qp[ss] = pq + (size_t)st * KC * 64 + lane;
+    sp[ss] = ps32 + (size_t)st * G * 8 + (j >> 1);
+    zp[ss] = pz + (size_t)st * G * 2 + (j >> 3);
+  }
+  const int hsh = (j & 1) * 16;
+  const int zsh = (j & 7) * 4;
+
+  u4 qb[U][SS];
+  h8 ab[U][4];
+  uint32_t sb[U][SS][GPC], zb[U][SS][GPC];
+  auto load = [&](int slot_u, int i) {
+    const int c = wave + i * WAVES;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ab[slot_u][t] = load_x_unit<ACT>(xr, perm, c * kChunkK + 32 * t + 8 * kq);
+#pragma unroll
+    for (int ss = 0; ss < SS; ++ss) {
+      qb[slot_u][ss] = __builtin_nontemporal_load(qp[ss] + (size_t)c * 64);
+#pragma unroll
+      for (int gl = 0; gl < GPC; ++gl) {
+        const int g = GPC == 1 ? (c * kChunkK) / gs : c * GPC + gl;
+        sb[slot_u][ss][gl] = sp[ss][(size_t)g * 8];
+        zb[slot_u][ss][gl] = zp[ss][(size_t)g * 2];
+      }
+    }
+  };
+  f4 tot[SS];
+#pragma unroll
+  for (int ss = 0; ss < SS; ++ss) tot[ss] = f4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t magic = kMagic;
+  auto consume = [&](int slot_u) {
+#pragma unroll
+    for (int ss = 0; ss < SS; ++ss)
+#pragma unroll
+      for (int gl = 0; gl < GPC; ++gl) {
+        h2 nz1024, nz64;
+        zero_consts(zb[slot_u][ss][gl], zsh, nz1024, nz64);
+        const float sc = (float)as_h((uint16_t)(sb[slot_u][ss][gl] >> hsh));
+        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < SPG; ++tt) {
+          const int t = gl * SPG + tt;
+          acc = mfma16(ab[slot_u][t], centered8(qb[slot_u][ss][t], nz1024, nz64, magic), acc);
+        }
+        tot[ss] += sc * acc;
+      }
+  };
+
+  // ring: the host gives every wave at least U chunks when U >= 2
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (U >= 2 || u < nch) load(u, u);
+  int i0 = 0;
+  for (; i0 + 2 * U <= nch; i0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      consume(u);
+      load(u, i0 + u + U);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = i0 + u;
+    if (i < nch) {
+      consume(u);
+      if (i + U < nch) load(u, i + U);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (i0 + U + u < nch) consume(u);
+
+  // fixed-order reduction across waves, then fp16 (+ bias) output
+  f4* red = reinterpret_cast<f4*>(smem);
+#pragma unroll
+  for (int ss = 0; ss < SS; ++ss) red[(wave * SS + ss) * 64 + lane] = tot[ss];
+  __syncthreads();
+  const float* redf = reinterpret_cast<const float*>(smem);
+  for (int idx = tid; idx < SS * 256; idx += T) {
+    const int ss = idx >> 8;
+    const int llo = idx & 15;
+    const int r = (idx >> 4) & 3;
+    const int lhi = (idx >> 6) & 3;
+    const int m = lhi * 4 + r;
+    const int st = s0 + ss;
+    if (m >= M || st >= NS) continue;
+    const int L = lhi * 16 + llo;
+    float sum = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; ++wv) sum += redf[((wv * SS + ss) * 64 + L) * 4 + r];
+    const int n = st * kStripN + llo;
+    _Float16 out = (_Float16)sum;
+    if (bias != nullptr) out = out + as_h(bias[n]);
+    y[(size_t)m * ldy + n] = h_bits(out);
+  }
+}
+
+template <int WAVES, int U, int SS, int GPC, bool ACT>
+static hipError_t launch_decode_reg_cfg(const GemmArgs& a, hipStream_t stream) {
+  const int NS = a.N / kStripN;
+  const dim3 grid((unsigned)((NS + SS - 1) / SS));
+  const size_t smem = (size_t)WAVES * SS * 64 * sizeof(f4);
+  decode_reg_kernel<WAVES, U, SS, GPC, ACT><<<grid, WAVES * 64, smem, stream>>>(
+      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
+      a.bias, a.y, a.ldy, a.K, a.N, a.gs, a.G);
+  return hipGetLastError();
+}
+
+template <int WAVES, int SS>
+static hipError_t launch_decode_reg_w(const GemmArgs& a, hipStream_t stream) {
+  const bool act = a.perm != nullptr;
+  const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
+  const int per_wave = (a.K / kChunkK) / WAVES;  // chunks of the shortest wave
+#define DW4_DREG(UU, GG)                                                             \
+  return act ? launch_decode_reg_cfg<WAVES, UU, SS, GG, true>(a, stream)             \
+             : launch_decode_reg_cfg<WAVES, UU, SS, GG, false>(a, stream)
+#define DW4_DREG_U(GG)                               \
+  if (per_wave >= 4) { DW4_DREG(4, GG); }            \
+  if (per_wave >= 2) { DW4_DREG(2, GG); }            \
+  DW4_DREG(1, GG)
+  if (gpc == 1) { DW4_DREG_U(1); }
+  if (gpc == 2) { DW4_DREG_U(2); }
+  DW4_DREG_U(4);
+#undef DW4_DREG_U
+#undef DW4_DREG
+}
+
+hipError_t launch_decode_reg(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
+  if (a.M > 16) return hipErrorInvalidValue;
+  if (p.waves == 16) return p.ss == 2 ? launch_decode_reg_w<16, 2>(a, stream)
+                                      : launch_decode_reg_w<16, 1>(a, stream);
+  return p.ss == 2 ? launch_decode_reg_w<8, 2>(a, stream) : launch_decode_reg_w<8, 1>(a, stream);
+}
+
+// ---------------------------------------------------------------------------
 // Prefill kernel, 16x16x32 MFMA form (used for 16-row tiles; larger tiles
 // use prefill32_kernel below): 4 waves; workgroup tile (16*MT2) rows x (64*S)
 // columns; waves split the columns (S strips each) and share the rows.
@@ -1168,6 +1339,7 @@ static hipError_t launch_decode_mt(const GemmArgs& a, const DecodePlan& p, float
 }
 
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream) {
+  if (p.reg) return launch_decode_reg(a, p, stream);
   switch ((a.M + 15) / 16) {
     case 1: return launch_decode_mt<1>(a, p, part, stream);
     case 2: return launch_decode_mt<2>(a, p, part, stream);

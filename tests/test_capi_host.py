@@ -106,12 +106,15 @@ def test_workspace_size_rules():
     assert _lib.workspace_size(1, 13824, 5120, 128, True) == 0
     # act-order gathers while staging: no gather buffer
     assert _lib.workspace_size(8, 4096, 4096, 128, True) == _lib.workspace_size(8, 4096, 4096, 128, False)
-    # M=16 x K=11008 does not fit one workgroup's LDS: fp32 split-K planes
-    # a split call's workspace: a fixed 16 KiB head of arrival counters, then
-    # whole fp32 partial planes [splits][M][N]
+    # M = 5..16 runs the register-fed decode kernel: K is never split
+    assert _lib.workspace_size(16, 11008, 4096, 128, False) == 0
+    assert _lib.workspace_size(8, 13824, 5120, 128, True) == 0
+    # M=4 x K=13824 does not fit the staged kernel's LDS share: fp32 split-K
+    # planes.  A split call's workspace: a fixed 16 KiB head of arrival
+    # counters, then whole fp32 partial planes [splits][M][N]
     head = 4096 * 4
-    ws = _lib.workspace_size(16, 11008, 4096, 128, False)
-    assert ws > head and (ws - head) % (16 * 4096 * 4) == 0
+    ws = _lib.workspace_size(4, 13824, 5120, 128, False)
+    assert ws > head and (ws - head) % (4 * 5120 * 4) == 0
     ws = _lib.workspace_size(256, 4096, 4096, 128, False)
     plane = 256 * 4096 * 4
     assert ws > head + plane and (ws - head) % plane == 0
