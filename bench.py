@@ -1,10 +1,10 @@
 #!/usr/bin/env python3
-"""W4A16 GEMM benchmark on one MI355X (the BASELINE metric).
+"""W4A16 GEMM benchmark on one MI355X: HBM GB/s at M=1, TFLOP/s at M=256, Llama-2-7B shapes.
 
 Step = one M=1 decode token through the 7 GPTQ projections (q, k, v, o,
 gate, up, down) of 8 Llama-2-7B layers -- one pipeline stage of the
-reference's split model (BASELINE config 5's layer count) with the
-config-2 quantisation (group 128, asymmetric zeros).  The 56 packed weight
+reference's split model (8 of the 32 decoder layers) with the
+GPTQ 4-bit quantisation (group 128, asymmetric zeros).  The 56 packed weight
 matrices (842 MB) are distinct, four times the 256 MB Infinity Cache, so
 every launch streams its weights from HBM.  The step is captured once into
 a HIP graph and replayed; timing uses HIP events on the replay stream.

@@ -159,7 +159,7 @@ def forward(x: np.ndarray, qweight: np.ndarray, qzeros: np.ndarray,
 
 
 def row_tolerance(y_ref: np.ndarray, rel: float = 2e-2) -> np.ndarray:
-    """Per-row bound ``rel * ||y_ref[m, :]||_inf`` (BASELINE parity rule)."""
+    """Per-row bound ``rel * ||y_ref[m, :]||_inf`` (the parity rule for GEMM outputs)."""
     y = np.asarray(y_ref, dtype=np.float64)
     return rel * np.max(np.abs(y), axis=-1, keepdims=True)
 

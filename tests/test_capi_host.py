@@ -167,7 +167,7 @@ def test_quantization_config():
 
 
 def test_algorithmic_bytes_match_baseline_table():
-    # values quoted in BASELINE.md section 3
+    # algorithmic bytes of the Llama-2-7B projections (K*N/2 + G*N/2 + 2*G*N + 2*M*K + 2*M*N)
     assert algorithmic_bytes(1, 4096, 4096, 128, False) == 8_732_672
     assert algorithmic_bytes(1, 4096, 4096, 128, False, count_zeros=False) == 8_667_136
     assert algorithmic_bytes(16, 4096, 11008, 128, False) == 23_908_352
@@ -176,7 +176,7 @@ def test_algorithmic_bytes_match_baseline_table():
     layer = sum(algorithmic_bytes(1, k, n, 128, False) for k, n in LLAMA2_7B_SHAPES.values())
     assert layer * 8 == 842_371_072  # 8-layer M=1 rotation used by bench.py
     layer8 = sum(algorithmic_bytes(8, k, n, 128, False) for k, n in LLAMA2_7B_SHAPES.values())
-    assert layer8 * 8 == 851_116_032  # BASELINE config 5 GEMM bytes per decode step
+    assert layer8 * 8 == 851_116_032  # 8-layer stage at M=8: GEMM bytes per decode step
 
 
 def test_synthetic_act_order_groups_uniform():

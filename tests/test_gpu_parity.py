@@ -1,6 +1,6 @@
 """GPU parity of the HIP W4A16 path against the pinned CPU oracle.
 
-Bars (BASELINE): dequantised fp16 weights bit-exact; GEMM outputs within
+Bars: dequantised fp16 weights bit-exact; GEMM outputs within
 max|y - y_ref| <= 2e-2 * ||y_ref row||_inf of a wide-accumulated reference.
 Every case prints its name before touching the GPU.
 """
@@ -21,7 +21,7 @@ from oracle import gptq
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-2  # BASELINE: max-abs error <= 2e-2 * ||row||_inf
+TOL = 2e-2  # max-abs error <= 2e-2 * ||row||_inf
 
 
 def say(msg: str) -> None:
@@ -165,11 +165,11 @@ def test_prefill_7b_shapes(hip_device, kn):
 def test_symmetric_c1(hip_device):
     lay, w = oracle_w(4096, 4096, 128, 0, True, False)
     q4 = build(lay, hip_device)
-    say("C1 symmetric 4096x4096 M=1")
+    say("symmetric (all zeros 8) 4096x4096 M=1")
     x = make_x(1, 4096, seed=0)
     y = q4.matmul(x.to(hip_device))
     torch.cuda.synchronize()
-    check_tol(y, gptq.gemm_ref(x.numpy(), w), "C1")
+    check_tol(y, gptq.gemm_ref(x.numpy(), w), "symmetric")
 
 
 @pytest.mark.parametrize("kn", [(5120, 5120), (13824, 5120), (5120, 13824)],
