@@ -62,8 +62,11 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
   if (splits <= 0) {
     const int cus = cu_count();  // one workgroup per CU at a time
     splits = tiles >= cus ? 1 : cus / tiles;
-    splits = std::min(splits, std::max(1, kc / 4));
-    splits = std::min(splits, 16);
+    // at least 8 chunks per split and at most 8 splits: the last split of a
+    // tile to arrive sums all the others' partials, so more splits lengthen
+    // that tail faster than they add parallelism (measured on 7B shapes)
+    splits = std::min(splits, std::max(1, kc / 8));
+    splits = std::min(splits, 8);
   }
   splits = std::max(1, std::min(splits, kc));
   // the launcher rounds to whole chunks per split
@@ -80,15 +83,15 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n) {
   return dw4::split_ws_bytes(p.splits, mt * nt * p.bm * p.bn);
 }
 
-bool use_decode(int path, int m) {
+bool use_decode(int path, int m, int n) {
   if (path == DW4_PATH_DECODE) return true;
   if (path == DW4_PATH_PREFILL) return false;
-  return m <= dw4::kDecodeAutoMaxM;
+  return dw4::auto_decode(m, n, cu_count());
 }
 
 size_t workspace_for(int path, int m, int k, int n, int group_size) {
   if (m <= 0) return 0;
-  if (use_decode(path, m)) {
+  if (use_decode(path, m, n)) {
     const dw4::DecodePlan p = dw4::plan_decode(m, k, n, group_size, cu_count());
     return dw4::split_ws_bytes(p.splits, (size_t)m * n);
   }
@@ -198,7 +201,7 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
   if (!x || !packed_qweight || !packed_zeros || !packed_scales || !y) return DW4_ERR_INVALID_ARG;
   if (ldx < k || ldy < n) return DW4_ERR_INVALID_ARG;
   if (!aligned16(x) || (ldx % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
-  const bool decode = use_decode(path, m);
+  const bool decode = use_decode(path, m, n);
   if (decode && m > dw4::kDecodeMaxM) return DW4_ERR_INVALID_ARG;
 
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -12,7 +12,8 @@ namespace dw4 {
 constexpr int kChunkK = 128;  // sorted rows per packed chunk
 constexpr int kStripN = 16;   // columns per strip
 constexpr int kDecodeMaxM = 64;      // four 16-row MFMA tiles
-constexpr int kDecodeAutoMaxM = 16;  // DW4_PATH_AUTO picks decode up to this M
+constexpr int kDecodeAutoMaxM = 24;        // DW4_PATH_AUTO picks decode up to this M,
+constexpr int kDecodeAutoMaxMNarrow = 32;  // and up to this M when strips <= CUs
 constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 #ifndef DW4_DECODE_UMAX
 #define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
@@ -78,15 +79,15 @@ inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
 inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus) {
   const int kc = k / kChunkK;
   const int strips = n / kStripN;
-  if (m >= kDecodeRegMinM && m <= 16) {
+  if (m >= kDecodeRegMinM && m <= kDecodeMaxM) {
     // register-fed: never split; two strips per workgroup share the A
-    // fragments when that still leaves a workgroup per CU; 16 waves when
-    // there are no more workgroups than CUs
+    // fragments when that still leaves a workgroup per CU; 16 waves for a
+    // single 16-row tile when there are no more workgroups than CUs
     DecodePlan r{1, kc, 8, 0};
     r.reg = true;
     r.ss = (strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
-    if ((strips + r.ss - 1) / r.ss <= cus && kc >= 32) r.waves = 16;
-    r.smem = (size_t)r.waves * r.ss * 64 * 16;
+    if (m <= 16 && r.ss == 1 && strips <= cus && kc >= 32) r.waves = 16;
+    r.smem = (size_t)r.waves * r.ss * ((m + 15) / 16) * 64 * 16;
     return r;
   }
   int waves = 8;
@@ -107,6 +108,13 @@ inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus) {
     }
   }
   return p;
+}
+
+// DW4_PATH_AUTO's choice.  The decode kernel streams each weight once but
+// every workgroup reads all M activation rows of its strips, so the prefill
+// kernel wins sooner when N has more strips than there are CUs.
+inline bool auto_decode(int m, int n, int cus) {
+  return m <= kDecodeAutoMaxM || (m <= kDecodeAutoMaxMNarrow && n / kStripN <= cus);
 }
 
 hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const uint16_t* scales,

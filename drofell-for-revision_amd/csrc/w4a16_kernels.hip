@@ -394,7 +394,7 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 }
 
 // ---------------------------------------------------------------------------
-// Decode kernel, register-fed form (5 <= M <= 16).  The staged kernel above
+// Decode kernel, register-fed form (5 <= M <= 64).  The staged kernel above
 // copies each strip's whole activation block into LDS before it starts; at
 // M = 16 that block (M * K * 2 bytes per strip) exceeds what three
 // workgroups per CU can hold, so the staged kernel splits K and runs in
@@ -403,7 +403,7 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 // and SS adjacent strips share them, so no LDS is needed until the final
 // cross-wave reduction and K is never split.
 // ---------------------------------------------------------------------------
-template <int WAVES, int U, int SS, int GPC, bool ACT>
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                   const int32_t* __restrict__ perm,
@@ -423,7 +423,9 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const int KC = K / kChunkK;
   const int nch = wave < KC ? (KC - wave + WAVES - 1) / WAVES : 0;
   // A rows: lanes past the last row read row M-1 (never stored)
-  const _Float16* xr = x + (size_t)min(j, M - 1) * ldx;
+  const _Float16* xr[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xr[mt] = x + (size_t)min(mt * 16 + j, M - 1) * ldx;
 
   const u4* qp[SS];
   const uint32_t* sp[SS];
@@ -439,12 +441,15 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const int zsh = (j & 7) * 4;
 
   u4 qb[U][SS];
-  h8 ab[U][4];
+  h8 ab[U][MT][4];
   uint32_t sb[U][SS][GPC], zb[U][SS][GPC];
   auto load = [&](int slot_u, int i) {
     const int c = wave + i * WAVES;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) ab[slot_u][t] = load_x_unit<ACT>(xr, perm, c * kChunkK + 32 * t + 8 * kq);
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ab[slot_u][mt][t] = load_x_unit<ACT>(xr[mt], perm, c * kChunkK + 32 * t + 8 * kq);
 #pragma unroll
     for (int ss = 0; ss < SS; ++ss) {
       qb[slot_u][ss] = __builtin_nontemporal_load(qp[ss] + (size_t)c * 64);
@@ -456,9 +461,11 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       }
     }
   };
-  f4 tot[SS];
+  f4 tot[SS][MT];
 #pragma unroll
-  for (int ss = 0; ss < SS; ++ss) tot[ss] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int ss = 0; ss < SS; ++ss)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) tot[ss][mt] = f4{0.f, 0.f, 0.f, 0.f};
   const uint32_t magic = kMagic;
   auto consume = [&](int slot_u) {
 #pragma unroll
@@ -468,13 +475,18 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
         h2 nz1024, nz64;
         zero_consts(zb[slot_u][ss][gl], zsh, nz1024, nz64);
         const float sc = (float)as_h((uint16_t)(sb[slot_u][ss][gl] >> hsh));
-        f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+        f4 acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int tt = 0; tt < SPG; ++tt) {
           const int t = gl * SPG + tt;
-          acc = mfma16(ab[slot_u][t], centered8(qb[slot_u][ss][t], nz1024, nz64, magic), acc);
+          const h8 b = centered8(qb[slot_u][ss][t], nz1024, nz64, magic);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16(ab[slot_u][mt][t], b, acc[mt]);
         }
-        tot[ss] += sc * acc;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) tot[ss][mt] += sc * acc[mt];
       }
   };
 
@@ -505,21 +517,25 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   // fixed-order reduction across waves, then fp16 (+ bias) output
   f4* red = reinterpret_cast<f4*>(smem);
 #pragma unroll
-  for (int ss = 0; ss < SS; ++ss) red[(wave * SS + ss) * 64 + lane] = tot[ss];
+  for (int ss = 0; ss < SS; ++ss)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[((wave * SS + ss) * MT + mt) * 64 + lane] = tot[ss][mt];
   __syncthreads();
   const float* redf = reinterpret_cast<const float*>(smem);
-  for (int idx = tid; idx < SS * 256; idx += T) {
-    const int ss = idx >> 8;
+  for (int idx = tid; idx < SS * MT * 256; idx += T) {
+    const int sm = idx >> 8;  // ss * MT + mt
+    const int ss = sm / MT;
+    const int mt = sm - ss * MT;
     const int llo = idx & 15;
     const int r = (idx >> 4) & 3;
     const int lhi = (idx >> 6) & 3;
-    const int m = lhi * 4 + r;
+    const int m = mt * 16 + lhi * 4 + r;
     const int st = s0 + ss;
     if (m >= M || st >= NS) continue;
     const int L = lhi * 16 + llo;
     float sum = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < WAVES; ++wv) sum += redf[((wv * SS + ss) * 64 + L) * 4 + r];
+    for (int wv = 0; wv < WAVES; ++wv) sum += redf[((wv * SS * MT + sm) * 64 + L) * 4 + r];
     const int n = st * kStripN + llo;
     _Float16 out = (_Float16)sum;
     if (bias != nullptr) out = out + as_h(bias[n]);
@@ -527,41 +543,73 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   }
 }
 
-template <int WAVES, int U, int SS, int GPC, bool ACT>
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT>
 static hipError_t launch_decode_reg_cfg(const GemmArgs& a, hipStream_t stream) {
   const int NS = a.N / kStripN;
   const dim3 grid((unsigned)((NS + SS - 1) / SS));
-  const size_t smem = (size_t)WAVES * SS * 64 * sizeof(f4);
-  decode_reg_kernel<WAVES, U, SS, GPC, ACT><<<grid, WAVES * 64, smem, stream>>>(
+  const size_t smem = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
+  decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT><<<grid, WAVES * 64, smem, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
       a.bias, a.y, a.ldy, a.K, a.N, a.gs, a.G);
   return hipGetLastError();
 }
 
-template <int WAVES, int SS>
-static hipError_t launch_decode_reg_w(const GemmArgs& a, hipStream_t stream) {
-  const bool act = a.perm != nullptr;
+// Deepest ring (chunks in flight per wave) that a variant holds without
+// spilling.  The A fragments of one chunk take 16 * MT registers per lane
+// (their act-order gathers more while in flight); 16-wave workgroups have
+// 128 registers per lane, 8-wave ones 256.
+constexpr int decode_reg_umax(int mt, int waves, int gpc, bool act) {
+  return waves == 16 ? ((act || gpc == 4) ? 2 : 4)
+         : mt == 1   ? 4
+         : act       ? 1
+                     : (mt == 2 ? 2 : 1);
+}
+
+// Ring depth U: the deepest allowed, at most the chunks of the shortest wave.
+template <int MT, int WAVES, int SS, int GPC, bool ACT>
+static hipError_t launch_decode_reg_u(const GemmArgs& a, hipStream_t stream) {
+  const int per_wave = (a.K / kChunkK) / WAVES;
+  constexpr int umax = decode_reg_umax(MT, WAVES, GPC, ACT);
+  if constexpr (umax >= 4) {
+    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT>(a, stream);
+  }
+  if constexpr (umax >= 2) {
+    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT>(a, stream);
+  }
+  return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT>(a, stream);
+}
+
+template <int MT, int WAVES, int SS, bool ACT>
+static hipError_t launch_decode_reg_g(const GemmArgs& a, hipStream_t stream) {
   const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
-  const int per_wave = (a.K / kChunkK) / WAVES;  // chunks of the shortest wave
-#define DW4_DREG(UU, GG)                                                             \
-  return act ? launch_decode_reg_cfg<WAVES, UU, SS, GG, true>(a, stream)             \
-             : launch_decode_reg_cfg<WAVES, UU, SS, GG, false>(a, stream)
-#define DW4_DREG_U(GG)                               \
-  if (per_wave >= 4) { DW4_DREG(4, GG); }            \
-  if (per_wave >= 2) { DW4_DREG(2, GG); }            \
-  DW4_DREG(1, GG)
-  if (gpc == 1) { DW4_DREG_U(1); }
-  if (gpc == 2) { DW4_DREG_U(2); }
-  DW4_DREG_U(4);
-#undef DW4_DREG_U
-#undef DW4_DREG
+  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT>(a, stream);
+  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT>(a, stream);
+  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT>(a, stream);
+}
+
+template <int MT, int WAVES, int SS>
+static hipError_t launch_decode_reg_w(const GemmArgs& a, hipStream_t stream) {
+  if (a.perm == nullptr) return launch_decode_reg_g<MT, WAVES, SS, false>(a, stream);
+  // act-order gathers for four tiles and two strips do not fit the registers
+  if constexpr (MT == 4 && SS == 2) return launch_decode_reg_g<MT, WAVES, 1, true>(a, stream);
+  else return launch_decode_reg_g<MT, WAVES, SS, true>(a, stream);
+}
+
+template <int MT>
+static hipError_t launch_decode_reg_mt(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
+  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2>(a, stream) : launch_decode_reg_w<MT, 8, 1>(a, stream);
 }
 
 hipError_t launch_decode_reg(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
-  if (a.M > 16) return hipErrorInvalidValue;
-  if (p.waves == 16) return p.ss == 2 ? launch_decode_reg_w<16, 2>(a, stream)
-                                      : launch_decode_reg_w<16, 1>(a, stream);
-  return p.ss == 2 ? launch_decode_reg_w<8, 2>(a, stream) : launch_decode_reg_w<8, 1>(a, stream);
+  if (a.M <= 16) {
+    if (p.waves == 16) return launch_decode_reg_w<1, 16, 1>(a, stream);  // planner: ss == 1
+    return launch_decode_reg_mt<1>(a, p, stream);
+  }
+  if (p.waves != 8) return hipErrorInvalidValue;
+  if (a.M <= 32) return launch_decode_reg_mt<2>(a, p, stream);
+  if (a.M <= 48) return launch_decode_reg_mt<3>(a, p, stream);
+  if (a.M <= 64) return launch_decode_reg_mt<4>(a, p, stream);
+  return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------

@@ -32,7 +32,9 @@ from . import _lib
 class TuningParams:
     # Flattened M at or below which the register-dequant decode kernel runs
     # (at most 64: four 16-row MFMA tiles); above it the prefill kernel runs.
-    DECODE_MAX_M: int = 16
+    # None leaves the choice to the library: decode up to M = 24, or up to
+    # M = 32 when N / 16 is at most the device's CU count.
+    DECODE_MAX_M: Optional[int] = None
     # Largest flattened M the shared workspace is sized for.  Larger calls
     # still run, with the prefill kernel unsplit along K.
     MAX_M: int = 4096
@@ -181,7 +183,10 @@ class Q4MatrixV2(object):
 
     # -- products ------------------------------------------------------------
     def _path(self, m: int) -> int:
-        if m <= min(self.tuning_params.DECODE_MAX_M, 64):
+        dmax = self.tuning_params.DECODE_MAX_M
+        if dmax is None:
+            return _lib.DW4_PATH_AUTO
+        if m <= min(dmax, 64):
             return _lib.DW4_PATH_DECODE
         return _lib.DW4_PATH_PREFILL
 

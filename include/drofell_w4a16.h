@@ -88,7 +88,7 @@ enum {
 
 /* Path selection for dw4_gemm_path(). */
 enum {
-  DW4_PATH_AUTO = 0,
+  DW4_PATH_AUTO = 0,     /* decode for M <= 24, or M <= 32 when N / 16 <= CUs */
   DW4_PATH_DECODE = 1,   /* register-dequant MFMA kernel, M <= 64 */
   DW4_PATH_PREFILL = 2   /* LDS-staged MFMA kernel, any M */
 };

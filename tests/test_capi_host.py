@@ -106,9 +106,16 @@ def test_workspace_size_rules():
     assert _lib.workspace_size(1, 13824, 5120, 128, True) == 0
     # act-order gathers while staging: no gather buffer
     assert _lib.workspace_size(8, 4096, 4096, 128, True) == _lib.workspace_size(8, 4096, 4096, 128, False)
-    # M = 5..16 runs the register-fed decode kernel: K is never split
+    # M = 5..64 runs the register-fed decode kernel: K is never split
     assert _lib.workspace_size(16, 11008, 4096, 128, False) == 0
     assert _lib.workspace_size(8, 13824, 5120, 128, True) == 0
+    # the automatic path takes decode up to M = 24, and up to M = 32 when
+    # N / 16 <= CUs (256 without a device); above, split-K prefill needs a
+    # workspace at these shapes
+    assert _lib.workspace_size(24, 4096, 11008, 128, False) == 0
+    assert _lib.workspace_size(32, 4096, 11008, 128, False) > 0
+    assert _lib.workspace_size(32, 11008, 4096, 128, False) == 0
+    assert _lib.workspace_size(40, 11008, 4096, 128, False) > 0
     # M=4 x K=13824 does not fit the staged kernel's LDS share: fp32 split-K
     # planes.  A split call's workspace: a fixed 16 KiB head of arrival
     # counters, then whole fp32 partial planes [splits][M][N]

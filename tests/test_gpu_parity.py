@@ -141,7 +141,7 @@ def test_decode_7b_shapes(hip_device, kn):
     k, n = kn
     lay, w = oracle_w(k, n, 128, 1000 + SHAPES_7B.index(kn), False, False)
     q4 = build(lay, hip_device)
-    for m in (1, 2, 4, 8, 16, 33, 64):
+    for m in (1, 2, 4, 8, 16, 20, 32, 33, 48, 64):
         say(f"decode 7B {k}x{n} M={m}")
         x = make_x(m, k, seed=m)
         y = q4.matmul(x.to(hip_device), path=_lib.DW4_PATH_DECODE)
@@ -179,7 +179,7 @@ def test_act_order_13b(hip_device, kn):
     lay, w = oracle_w(k, n, 128, 2000 + k + n, False, True)
     q4 = build(lay, hip_device)
     assert q4.use_act
-    for m in (1, 8, 64):
+    for m in (1, 8, 24, 64):
         for path in (_lib.DW4_PATH_DECODE, _lib.DW4_PATH_PREFILL):
             say(f"act-order 13B {k}x{n} M={m} path={path}")
             x = make_x(m, k, seed=m + 11)
@@ -194,7 +194,7 @@ def test_group_sizes(hip_device, g):
     for act in (False, True):
         lay, w = oracle_w(k, n, g, 3000 + g, False, act)
         q4 = build(lay, hip_device)
-        for m in (1, 5, 33, 100):
+        for m in (1, 5, 24, 33, 64, 100):
             for path in ((_lib.DW4_PATH_DECODE, _lib.DW4_PATH_PREFILL) if m <= 64
                          else (_lib.DW4_PATH_PREFILL,)):
                 say(f"group g={g} act={act} M={m} path={path}")
@@ -382,12 +382,18 @@ def test_errors_surface(hip_device):
                       q4.scales.data_ptr(), None, None, y.data_ptr(), 4096, None, 0, None)
     assert st == _lib.DW4_ERR_UNSUPPORTED
     say("errors: split decode without workspace")
-    # M=64 x K=4096 activations exceed one workgroup's LDS: fp32 split-K partials needed
-    xs = torch.zeros(64, 4096, dtype=torch.float16, device=hip_device)
-    ys = torch.empty(64, 4096, dtype=torch.float16, device=hip_device)
-    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 64, 4096, 4096, 128, xs.data_ptr(), 4096,
-                           q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(), None,
-                           None, ys.data_ptr(), 4096, None, 0, None)
+    # M=4 x K=13824 activations exceed one workgroup's LDS share at N=5120:
+    # fp32 split-K partials needed (all-zero packed buffers of the right sizes)
+    kb, nb = 13824, 5120
+    pq = torch.zeros(kb // 8 * nb, dtype=torch.int32, device=hip_device)
+    pz = torch.zeros(kb // 128 * nb // 8, dtype=torch.int32, device=hip_device)
+    ps = torch.zeros(kb // 128 * nb, dtype=torch.float16, device=hip_device)
+    xs = torch.zeros(4, kb, dtype=torch.float16, device=hip_device)
+    ys = torch.empty(4, nb, dtype=torch.float16, device=hip_device)
+    assert _lib.workspace_size(4, kb, nb, 128, False) > 0
+    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 4, kb, nb, 128, xs.data_ptr(), kb,
+                           pq.data_ptr(), pz.data_ptr(), ps.data_ptr(), None,
+                           None, ys.data_ptr(), nb, None, 0, None)
     assert st == _lib.DW4_ERR_WORKSPACE
     say("errors: misaligned view goes through an aligned copy")
     xv = x[:, 1:4097]
