@@ -262,3 +262,163 @@ int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Decoder-stage calls
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_item(const dw4_item* it) {
+  if (it == nullptr) return DW4_ERR_INVALID_ARG;
+  const int st = check_shape(it->k, it->n, it->group_size);
+  if (st != DW4_OK) return st;
+  if (!it->packed_qweight || !it->packed_zeros || !it->packed_scales) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(it->packed_qweight)) return DW4_ERR_MISALIGNED;
+  return DW4_OK;
+}
+
+int check_output(const dw4_item* it) {
+  if (it->y == nullptr || it->ldy < it->n) return DW4_ERR_INVALID_ARG;
+  return DW4_OK;
+}
+
+int check_x(const uint16_t* x, int64_t ldx, int k) {
+  if (x == nullptr || ldx < k) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(x) || (ldx % 8) != 0) return DW4_ERR_MISALIGNED;
+  return DW4_OK;
+}
+
+dw4::GemmArgs args_of(int m, const uint16_t* x, int64_t ldx, const dw4_item* it) {
+  dw4::GemmArgs a;
+  a.M = m;
+  a.K = it->k;
+  a.N = it->n;
+  a.gs = it->group_size;
+  a.G = it->k / it->group_size;
+  a.x = x;
+  a.ldx = ldx;
+  a.pq = reinterpret_cast<const uint32_t*>(it->packed_qweight);
+  a.pz = reinterpret_cast<const uint32_t*>(it->packed_zeros);
+  a.ps = it->packed_scales;
+  a.perm = it->perm;
+  a.bias = it->bias;
+  a.y = it->y;
+  a.ldy = it->ldy;
+  return a;
+}
+
+int gemm_item(int m, const uint16_t* x, int64_t ldx, const dw4_item* it, void* ws, size_t wsb,
+              void* stream) {
+  return dw4_gemm_path(DW4_PATH_AUTO, 0, m, it->k, it->n, it->group_size, x, ldx,
+                       it->packed_qweight, it->packed_zeros, it->packed_scales, it->perm, it->bias,
+                       it->y, it->ldy, ws, wsb, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, int64_t ldx,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (count < 1 || count > dw4::kGroupMax || items == nullptr || m < 0) return DW4_ERR_INVALID_ARG;
+  int n_total = 0;
+  for (int i = 0; i < count; ++i) {
+    int st = check_item(&items[i]);
+    if (st == DW4_OK) st = check_output(&items[i]);
+    if (st != DW4_OK) return st;
+    if (items[i].k != items[0].k || items[i].group_size != items[0].group_size ||
+        (items[i].perm == nullptr) != (items[0].perm == nullptr))
+      return DW4_ERR_INVALID_ARG;
+    n_total += items[i].n;
+  }
+  if (m == 0) return DW4_OK;
+  const int st = check_x(x, ldx, items[0].k);
+  if (st != DW4_OK) return st;
+  const int cus = cu_count();
+  if (m <= dw4::kDecodeMaxM && dw4::auto_decode(m, n_total, cus)) {
+    const dw4::DecodePlan plan = dw4::plan_decode(m, items[0].k, n_total, items[0].group_size, cus);
+    if (plan.splits == 1) {
+      dw4::GroupArgs g{};
+      g.count = count;
+      for (int i = 0; i < count; ++i) g.a[i] = args_of(m, x, ldx, &items[i]);
+      return status_of(dw4::launch_decode_group(g, plan, static_cast<hipStream_t>(stream)));
+    }
+  }
+  for (int i = 0; i < count; ++i) {
+    const int r = gemm_item(m, x, ldx, &items[i], workspace, workspace_bytes, stream);
+    if (r != DW4_OK) return r;
+  }
+  return DW4_OK;
+}
+
+int dw4_gemm_silu_mul(int m, const uint16_t* x, int64_t ldx, const dw4_item* gate,
+                      const dw4_item* up, uint16_t* h, int64_t ldh, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  int st = check_item(gate);
+  if (st == DW4_OK) st = check_item(up);
+  if (st != DW4_OK) return st;
+  if (m < 0 || gate->k != up->k || gate->n != up->n || gate->group_size != up->group_size ||
+      (gate->perm == nullptr) != (up->perm == nullptr))
+    return DW4_ERR_INVALID_ARG;
+  if (h == nullptr || ldh < gate->n) return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  st = check_x(x, ldx, gate->k);
+  if (st != DW4_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m <= dw4::kPairMaxM && gate->perm == up->perm &&
+      dw4::auto_decode(m, 2 * gate->n, cu_count())) {
+    dw4::GroupArgs g{};
+    g.count = 2;
+    g.a[0] = args_of(m, x, ldx, gate);
+    g.a[1] = args_of(m, x, ldx, up);
+    return status_of(dw4::launch_decode_pair(g, h, ldh, s));
+  }
+  st = check_output(gate);
+  if (st == DW4_OK) st = check_output(up);
+  if (st != DW4_OK) return st;
+  st = gemm_item(m, x, ldx, gate, workspace, workspace_bytes, stream);
+  if (st == DW4_OK) st = gemm_item(m, x, ldx, up, workspace, workspace_bytes, stream);
+  if (st != DW4_OK) return st;
+  return status_of(dw4::launch_silu_mul(gate->y, gate->ldy, up->y, up->ldy, h, ldh, m, gate->n, s));
+}
+
+int dw4_rms_norm(int m, int k, const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                 uint16_t* y, int64_t ldy, void* stream) {
+  if (m < 0 || k <= 0 || !x || !w || !y || ldx < k || ldy < k || !(eps >= 0.0f))
+    return DW4_ERR_INVALID_ARG;
+  if (k % 8 != 0) return DW4_ERR_UNSUPPORTED;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y) || ldx % 8 != 0 || ldy % 8 != 0)
+    return DW4_ERR_MISALIGNED;
+  if (m == 0) return DW4_OK;
+  return status_of(dw4::launch_rms_norm(x, ldx, w, eps, y, ldy, m, k, static_cast<hipStream_t>(stream)));
+}
+
+int dw4_attention_qkv_stage(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w,
+                            float eps, uint16_t* rms, int64_t ldr, const dw4_item* q,
+                            const dw4_item* k, const dw4_item* v, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (q == nullptr || k == nullptr || v == nullptr) return DW4_ERR_INVALID_ARG;
+  const dw4_item items[3] = {*q, *k, *v};
+  int st = dw4_rms_norm(m, q->k, x, ldx, norm_w, eps, rms, ldr, stream);
+  if (st != DW4_OK) return st;
+  return dw4_gemm_group(3, items, m, rms, ldr, workspace, workspace_bytes, stream);
+}
+
+int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
+                    uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+                    const dw4_item* down, void* workspace, size_t workspace_bytes, void* stream) {
+  if (gate == nullptr || up == nullptr || down == nullptr) return DW4_ERR_INVALID_ARG;
+  int st = check_item(down);
+  if (st == DW4_OK) st = check_output(down);
+  if (st == DW4_OK) st = check_output(gate);
+  if (st != DW4_OK) return st;
+  if (down->k != gate->n) return DW4_ERR_INVALID_ARG;
+  st = dw4_rms_norm(m, gate->k, x, ldx, norm_w, eps, rms, ldr, stream);
+  if (st == DW4_OK)
+    st = dw4_gemm_silu_mul(m, rms, ldr, gate, up, gate->y, gate->ldy, workspace, workspace_bytes,
+                           stream);
+  if (st != DW4_OK) return st;
+  return gemm_item(m, gate->y, gate->ldy, down, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

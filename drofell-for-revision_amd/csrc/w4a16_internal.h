@@ -41,6 +41,29 @@ struct GemmArgs {
   int64_t ldy;
 };
 
+// Matrices launched together.  They share x, M, K and the group size; each
+// has its own packed buffers, perm, bias and output.  Decode launches give
+// item i the workgroups [wg0[i], wg0[i+1]).
+constexpr int kGroupMax = 4;
+struct GroupArgs {
+  int count;
+  GemmArgs a[kGroupMax];
+};
+
+// Kernel-side table of a grouped launch (passed by value).
+struct Items {
+  const uint32_t* pq[kGroupMax];
+  const uint32_t* pz[kGroupMax];
+  const uint16_t* ps[kGroupMax];
+  const int32_t* perm[kGroupMax];
+  const uint16_t* bias[kGroupMax];
+  uint16_t* y[kGroupMax];
+  int64_t ldy[kGroupMax];
+  int n[kGroupMax];
+  int wg0[kGroupMax + 1];
+  int count;
+};
+
 // Prefill launch: row tile bm (16: 16x16x32 MFMA kernel; 32, 64, 128:
 // 32x32x16 MFMA kernel), column tile bn (128 or 256), split-K factor.
 struct PrefillPlan {
@@ -121,7 +144,19 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
                          const int32_t* perm, uint32_t* pq, uint32_t* pz, uint16_t* ps,
                          int K, int N, int G, hipStream_t stream);
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream);
-hipError_t launch_decode_reg(const GemmArgs& a, const DecodePlan& p, hipStream_t stream);
+hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
+// One launch over every strip of g's matrices (decode plan with one split).
+hipError_t launch_decode_group(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
+// h[m, n] = fp16(silu(fp16(x @ W0 + b0)) * fp16(x @ W1 + b1)) for two matrices of equal N
+// and equal perm (gate, up): one register-fed launch, workgroup s holding strip s of both.
+constexpr int kPairMaxM = 32;  // largest M of launch_decode_pair
+hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipStream_t stream);
+// Elementwise h = fp16(silu(g) * u) over [m, n] (row strides ldg, ldu, ldh).
+hipError_t launch_silu_mul(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
+                           uint16_t* h, int64_t ldh, int m, int n, hipStream_t stream);
+// y = fp16(x * w * rsqrt(mean(x^2) + eps)) per row of [m, k].
+hipError_t launch_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                           uint16_t* y, int64_t ldy, int m, int k, hipStream_t stream);
 // Workspace of a split-K call: a fixed head of kSplitCounters int32 arrival
 // counters (one per prefill output tile; zero before the first call and left
 // zero by every call), then one fp32 partial plane per split: [M][N] for the

@@ -157,8 +157,21 @@ __device__ __forceinline__ h8 load_x_unit(const _Float16* __restrict__ row,
   return *(const h8*)(row + k);
 }
 
+// Entry i of a per-item array of a grouped launch (item index wave-uniform).
+template <typename T, int L>
+__device__ __forceinline__ T pick(const T (&v)[L], int i) {
+  static_assert(kGroupMax == 4 && L >= 4, "pick() selects among four items");
+  return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
+// Item that owns workgroup b (wg0 ascending).
+__device__ __forceinline__ int item_of(const Items& d, int b) {
+  return (d.count > 1 && b >= d.wg0[1]) + (d.count > 2 && b >= d.wg0[2]) +
+         (d.count > 3 && b >= d.wg0[3]);
+}
+
 // ---------------------------------------------------------------------------
-// Decode kernel (M <= 64).  Grid: (N/16 strips) x (K splits).  Each wave
+// Decode kernel (M <= 64).  Grid: (N/16 strips of every item) x (K splits).  Each wave
 // owns the interleaved 128-row chunks lc = wave + i*WAVES of its workgroup's
 // K range.  It stages the activation slices (gathered for act-order) and the
 // scale/zero records of exactly those chunks into a private LDS region and
@@ -176,14 +189,20 @@ constexpr int kLdx = kChunkK + 8;  // halfs per staged activation row (16-byte p
 
 template <int MT, int WAVES, int U, bool G128, bool ACT>
 __global__ void __launch_bounds__(WAVES * 64)
-decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t* __restrict__ perm,
-              const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
-              const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
-              uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part, int K, int N,
-              int gs, int G, int cps) {
+decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
+              float* __restrict__ part, int K, int gs, int G, int cps) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
-  const int s = blockIdx.x;
+  const int item = item_of(d, blockIdx.x);
+  const int s = blockIdx.x - pick(d.wg0, item);  // strip within the item
+  const int N = pick(d.n, item);
+  const int32_t* __restrict__ perm = pick(d.perm, item);
+  const u4* __restrict__ pq = reinterpret_cast<const u4*>(pick(d.pq, item));
+  const uint32_t* __restrict__ pz = pick(d.pz, item);
+  const uint32_t* __restrict__ ps32 = reinterpret_cast<const uint32_t*>(pick(d.ps, item));
+  const uint16_t* __restrict__ bias = pick(d.bias, item);
+  uint16_t* __restrict__ y = pick(d.y, item);
+  const int64_t ldy = pick(d.ldy, item);
   const int split = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -402,19 +421,24 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const int32_t*
 // per 32-row k-step, from L2) into the same register ring as the weights,
 // and SS adjacent strips share them, so no LDS is needed until the final
 // cross-wave reduction and K is never split.
+// PAIR (SS = 2): workgroup s holds strip s of item 0 (gate) and of item 1
+// (up), which share perm, and writes fp16(silu(gate) * up) to item 0's
+// output; the two products never reach memory.
 // ---------------------------------------------------------------------------
-template <int MT, int WAVES, int U, int SS, int GPC, bool ACT>
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
+
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, bool PAIR>
 __global__ void __launch_bounds__(WAVES * 64)
-decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
-                  const int32_t* __restrict__ perm,
-                  const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
-                  const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
-                  uint16_t* __restrict__ y, int64_t ldy, int K, int N, int gs, int G) {
+decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d, int K,
+                  int gs, int G) {
+  static_assert(!PAIR || SS == 2, "a pair workgroup holds one strip of each matrix");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
   constexpr int SPG = 4 / GPC;  // 32-row k-steps per group
-  const int s0 = blockIdx.x * SS;
-  const int NS = N / kStripN;
+  const int item = PAIR ? 0 : item_of(d, blockIdx.x);
+  const int s0 = PAIR ? (int)blockIdx.x : ((int)blockIdx.x - pick(d.wg0, item)) * SS;
+  const int NS = pick(d.n, item) / kStripN;
+  const int32_t* __restrict__ perm = pick(d.perm, item);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -432,10 +456,11 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const uint32_t* zp[SS];
 #pragma unroll
   for (int ss = 0; ss < SS; ++ss) {
-    const int st = min(s0 + ss, NS - 1);
-    qp[ss] = pq + (size_t)st * KC * 64 + lane;
-    sp[ss] = ps32 + (size_t)st * G * 8 + (j >> 1);
-    zp[ss] = pz + (size_t)st * G * 2 + (j >> 3);
+    const int src = PAIR ? ss : item;
+    const int st = PAIR ? s0 : min(s0 + ss, NS - 1);
+    qp[ss] = reinterpret_cast<const u4*>(pick(d.pq, src)) + (size_t)st * KC * 64 + lane;
+    sp[ss] = reinterpret_cast<const uint32_t*>(pick(d.ps, src)) + (size_t)st * G * 8 + (j >> 1);
+    zp[ss] = pick(d.pz, src) + (size_t)st * G * 2 + (j >> 3);
   }
   const int hsh = (j & 1) * 16;
   const int zsh = (j & 7) * 4;
@@ -522,35 +547,83 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     for (int mt = 0; mt < MT; ++mt) red[((wave * SS + ss) * MT + mt) * 64 + lane] = tot[ss][mt];
   __syncthreads();
   const float* redf = reinterpret_cast<const float*>(smem);
-  for (int idx = tid; idx < SS * MT * 256; idx += T) {
-    const int sm = idx >> 8;  // ss * MT + mt
-    const int ss = sm / MT;
-    const int mt = sm - ss * MT;
-    const int llo = idx & 15;
-    const int r = (idx >> 4) & 3;
-    const int lhi = (idx >> 6) & 3;
-    const int m = mt * 16 + lhi * 4 + r;
-    const int st = s0 + ss;
-    if (m >= M || st >= NS) continue;
-    const int L = lhi * 16 + llo;
+  auto wave_sum = [&](int sm, int L, int r) {
     float sum = 0.f;
 #pragma unroll
     for (int wv = 0; wv < WAVES; ++wv) sum += redf[((wv * SS * MT + sm) * 64 + L) * 4 + r];
-    const int n = st * kStripN + llo;
-    _Float16 out = (_Float16)sum;
-    if (bias != nullptr) out = out + as_h(bias[n]);
-    y[(size_t)m * ldy + n] = h_bits(out);
+    return sum;
+  };
+  if constexpr (PAIR) {
+    const uint16_t* __restrict__ bg = d.bias[0];
+    const uint16_t* __restrict__ bu = d.bias[1];
+    uint16_t* __restrict__ h = d.y[0];
+    const int64_t ldh = d.ldy[0];
+    for (int idx = tid; idx < MT * 256; idx += T) {
+      const int mt = idx >> 8;
+      const int llo = idx & 15;
+      const int r = (idx >> 4) & 3;
+      const int lhi = (idx >> 6) & 3;
+      const int m = mt * 16 + lhi * 4 + r;
+      if (m >= M) continue;
+      const int L = lhi * 16 + llo;
+      const int n = s0 * kStripN + llo;
+      _Float16 g = (_Float16)wave_sum(mt, L, r);
+      _Float16 u = (_Float16)wave_sum(MT + mt, L, r);
+      if (bg != nullptr) g = g + as_h(bg[n]);
+      if (bu != nullptr) u = u + as_h(bu[n]);
+      h[(size_t)m * ldh + n] = h_bits((_Float16)(silu_f32((float)g) * (float)u));
+    }
+  } else {
+    const uint16_t* __restrict__ bias = pick(d.bias, item);
+    uint16_t* __restrict__ y = pick(d.y, item);
+    const int64_t ldy = pick(d.ldy, item);
+    for (int idx = tid; idx < SS * MT * 256; idx += T) {
+      const int sm = idx >> 8;  // ss * MT + mt
+      const int ss = sm / MT;
+      const int mt = sm - ss * MT;
+      const int llo = idx & 15;
+      const int r = (idx >> 4) & 3;
+      const int lhi = (idx >> 6) & 3;
+      const int m = mt * 16 + lhi * 4 + r;
+      const int st = s0 + ss;
+      if (m >= M || st >= NS) continue;
+      const int L = lhi * 16 + llo;
+      const int n = st * kStripN + llo;
+      _Float16 out = (_Float16)wave_sum(sm, L, r);
+      if (bias != nullptr) out = out + as_h(bias[n]);
+      y[(size_t)m * ldy + n] = h_bits(out);
+    }
   }
 }
 
-template <int MT, int WAVES, int U, int SS, int GPC, bool ACT>
-static hipError_t launch_decode_reg_cfg(const GemmArgs& a, hipStream_t stream) {
-  const int NS = a.N / kStripN;
-  const dim3 grid((unsigned)((NS + SS - 1) / SS));
+// Item table of a launch: item i gets ceil(strips_i / ss) workgroups.
+static Items make_items(const GroupArgs& g, int ss) {
+  Items d{};
+  d.count = g.count;
+  d.wg0[0] = 0;
+  for (int i = 0; i < kGroupMax; ++i) {
+    const GemmArgs& a = g.a[i < g.count ? i : 0];
+    d.pq[i] = a.pq;
+    d.pz[i] = a.pz;
+    d.ps[i] = a.ps;
+    d.perm[i] = a.perm;
+    d.bias[i] = a.bias;
+    d.y[i] = a.y;
+    d.ldy[i] = a.ldy;
+    d.n[i] = a.N;
+    const int wgs = i < g.count ? (a.N / kStripN + ss - 1) / ss : 0;
+    d.wg0[i + 1] = d.wg0[i] + wgs;
+  }
+  return d;
+}
+
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, bool PAIR>
+static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, hipStream_t stream) {
+  const GemmArgs& a = g.a[0];
+  const dim3 grid((unsigned)(PAIR ? a.N / kStripN : d.wg0[d.count]));
   const size_t smem = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
-  decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT><<<grid, WAVES * 64, smem, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
-      a.bias, a.y, a.ldy, a.K, a.N, a.gs, a.G);
+  decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT, PAIR><<<grid, WAVES * 64, smem, stream>>>(
+      (const _Float16*)a.x, a.ldx, a.M, d, a.K, a.gs, a.G);
   return hipGetLastError();
 }
 
@@ -566,49 +639,72 @@ constexpr int decode_reg_umax(int mt, int waves, int gpc, bool act) {
 }
 
 // Ring depth U: the deepest allowed, at most the chunks of the shortest wave.
-template <int MT, int WAVES, int SS, int GPC, bool ACT>
-static hipError_t launch_decode_reg_u(const GemmArgs& a, hipStream_t stream) {
-  const int per_wave = (a.K / kChunkK) / WAVES;
+template <int MT, int WAVES, int SS, int GPC, bool ACT, bool PAIR>
+static hipError_t launch_decode_reg_u(const GroupArgs& g, const Items& d, hipStream_t stream) {
+  const int per_wave = (g.a[0].K / kChunkK) / WAVES;
   constexpr int umax = decode_reg_umax(MT, WAVES, GPC, ACT);
   if constexpr (umax >= 4) {
-    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT>(a, stream);
+    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT, PAIR>(g, d, stream);
   }
   if constexpr (umax >= 2) {
-    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT>(a, stream);
+    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT, PAIR>(g, d, stream);
   }
-  return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT>(a, stream);
+  // 16 waves are planned only where every wave gets two chunks or more
+  if constexpr (WAVES == 16) return hipErrorInvalidValue;
+  else return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT, PAIR>(g, d, stream);
 }
 
-template <int MT, int WAVES, int SS, bool ACT>
-static hipError_t launch_decode_reg_g(const GemmArgs& a, hipStream_t stream) {
-  const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
-  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT>(a, stream);
-  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT>(a, stream);
-  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT>(a, stream);
+template <int MT, int WAVES, int SS, bool ACT, bool PAIR>
+static hipError_t launch_decode_reg_g(const GroupArgs& g, const Items& d, hipStream_t stream) {
+  const int gs = g.a[0].gs;
+  const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
+  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, PAIR>(g, d, stream);
+  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, PAIR>(g, d, stream);
+  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT, PAIR>(g, d, stream);
 }
 
-template <int MT, int WAVES, int SS>
-static hipError_t launch_decode_reg_w(const GemmArgs& a, hipStream_t stream) {
-  if (a.perm == nullptr) return launch_decode_reg_g<MT, WAVES, SS, false>(a, stream);
+template <int MT, int WAVES, int SS, bool PAIR = false>
+static hipError_t launch_decode_reg_w(const GroupArgs& g, hipStream_t stream) {
+  if (g.a[0].perm == nullptr) {
+    const Items d = make_items(g, PAIR ? 1 : SS);
+    return launch_decode_reg_g<MT, WAVES, SS, false, PAIR>(g, d, stream);
+  }
   // act-order gathers for four tiles and two strips do not fit the registers
-  if constexpr (MT == 4 && SS == 2) return launch_decode_reg_g<MT, WAVES, 1, true>(a, stream);
-  else return launch_decode_reg_g<MT, WAVES, SS, true>(a, stream);
+  if constexpr (MT == 4 && SS == 2 && !PAIR) {
+    const Items d = make_items(g, 1);
+    return launch_decode_reg_g<MT, WAVES, 1, true, false>(g, d, stream);
+  } else {
+    const Items d = make_items(g, PAIR ? 1 : SS);
+    return launch_decode_reg_g<MT, WAVES, SS, true, PAIR>(g, d, stream);
+  }
 }
 
 template <int MT>
-static hipError_t launch_decode_reg_mt(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
-  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2>(a, stream) : launch_decode_reg_w<MT, 8, 1>(a, stream);
+static hipError_t launch_decode_reg_mt(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
+  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2>(g, stream) : launch_decode_reg_w<MT, 8, 1>(g, stream);
 }
 
-hipError_t launch_decode_reg(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
-  if (a.M <= 16) {
-    if (p.waves == 16) return launch_decode_reg_w<1, 16, 1>(a, stream);  // planner: ss == 1
-    return launch_decode_reg_mt<1>(a, p, stream);
+hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
+  const int M = g.a[0].M;
+  if (M <= 16) {
+    if (p.waves == 16) return launch_decode_reg_w<1, 16, 1>(g, stream);  // planner: ss == 1
+    return launch_decode_reg_mt<1>(g, p, stream);
   }
   if (p.waves != 8) return hipErrorInvalidValue;
-  if (a.M <= 32) return launch_decode_reg_mt<2>(a, p, stream);
-  if (a.M <= 48) return launch_decode_reg_mt<3>(a, p, stream);
-  if (a.M <= 64) return launch_decode_reg_mt<4>(a, p, stream);
+  if (M <= 32) return launch_decode_reg_mt<2>(g, p, stream);
+  if (M <= 48) return launch_decode_reg_mt<3>(g, p, stream);
+  if (M <= 64) return launch_decode_reg_mt<4>(g, p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipStream_t stream) {
+  if (g.count != 2 || g.a[0].N != g.a[1].N || g.a[0].perm != g.a[1].perm) return hipErrorInvalidValue;
+  GroupArgs gp = g;
+  gp.a[0].y = h;  // the pair's output goes where item 0's would
+  gp.a[0].ldy = ldh;
+  const int M = g.a[0].M;
+  if (M <= 16) return launch_decode_reg_w<1, 8, 2, true>(gp, stream);
+  if (M <= kPairMaxM) return launch_decode_reg_w<2, 8, 2, true>(gp, stream);
   return hipErrorInvalidValue;
 }
 
@@ -1321,9 +1417,12 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
 }
 
 template <int MT, int WAVES, int U, bool G128, bool ACT>
-static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, float* part,
+static hipError_t launch_decode_cfg(const GroupArgs& g, const DecodePlan& p, float* part,
                                     hipStream_t stream) {
-  const dim3 grid(a.N / kStripN, p.splits);
+  const GemmArgs& a = g.a[0];
+  if (p.splits > 1 && g.count != 1) return hipErrorInvalidValue;  // planes of one matrix
+  const Items d = make_items(g, 1);
+  const dim3 grid((unsigned)d.wg0[g.count], p.splits);
   if (p.smem > 64 * 1024) {
     static bool raised = false;  // idempotent attribute; races only repeat it
     if (!raised) {
@@ -1335,8 +1434,7 @@ static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, floa
     }
   }
   decode_kernel<MT, WAVES, U, G128, ACT><<<grid, WAVES * 64, p.smem, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
-      a.bias, a.y, a.ldy, part, a.K, a.N, a.gs, a.G, p.cps);
+      (const _Float16*)a.x, a.ldx, a.M, d, part, a.K, a.gs, a.G, p.cps);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.splits == 1) return err;
   const size_t total = (size_t)a.M * a.N;
@@ -1346,7 +1444,7 @@ static hipError_t launch_decode_cfg(const GemmArgs& a, const DecodePlan& p, floa
 }
 
 template <int MT, int WAVES, bool G128>
-static hipError_t launch_decode_g(const GemmArgs& a, const DecodePlan& p, float* part,
+static hipError_t launch_decode_g(const GroupArgs& g, const DecodePlan& p, float* part,
                                   hipStream_t stream) {
   // Ring depth: the largest of 8, 4, 2 that every wave can fill (the shortest
   // wave gets floor(chunks / waves) chunks); 1 (conditional prologue)
@@ -1355,13 +1453,14 @@ static hipError_t launch_decode_g(const GemmArgs& a, const DecodePlan& p, float*
   // (measured: deeper rings only lengthen the initial request burst that
   // every wave's activation loads queue behind)
   constexpr int UMAX = G128 ? (WAVES >= 16 ? 2 : kDecodeUMax) : (WAVES >= 16 ? 2 : 4);
+  const GemmArgs& a = g.a[0];
   const int KC = a.K / kChunkK;
   const int last = min(p.cps, KC - (p.splits - 1) * p.cps);  // shortest split
   const int per_wave = last / WAVES;
   const bool act = a.perm != nullptr;
 #define DW4_DECODE_U(UU)                                                                  \
-  return act ? launch_decode_cfg<MT, WAVES, UU, G128, true>(a, p, part, stream)            \
-             : launch_decode_cfg<MT, WAVES, UU, G128, false>(a, p, part, stream)
+  return act ? launch_decode_cfg<MT, WAVES, UU, G128, true>(g, p, part, stream)            \
+             : launch_decode_cfg<MT, WAVES, UU, G128, false>(g, p, part, stream)
   if (UMAX >= 8 && per_wave >= 8) { DW4_DECODE_U(UMAX >= 8 ? 8 : 1); }
   if (UMAX >= 4 && per_wave >= 4) { DW4_DECODE_U(UMAX >= 4 ? 4 : 1); }
   if (per_wave >= 2) { DW4_DECODE_U(2); }
@@ -1370,31 +1469,44 @@ static hipError_t launch_decode_g(const GemmArgs& a, const DecodePlan& p, float*
 }
 
 template <int MT, int WAVES>
-static hipError_t launch_decode_w(const GemmArgs& a, const DecodePlan& p, float* part,
+static hipError_t launch_decode_w(const GroupArgs& g, const DecodePlan& p, float* part,
                                   hipStream_t stream) {
-  if ((a.gs % kChunkK) == 0) return launch_decode_g<MT, WAVES, true>(a, p, part, stream);
-  return launch_decode_g<MT, WAVES, false>(a, p, part, stream);
+  if ((g.a[0].gs % kChunkK) == 0) return launch_decode_g<MT, WAVES, true>(g, p, part, stream);
+  return launch_decode_g<MT, WAVES, false>(g, p, part, stream);
 }
 
 template <int MT>
-static hipError_t launch_decode_mt(const GemmArgs& a, const DecodePlan& p, float* part,
+static hipError_t launch_decode_mt(const GroupArgs& g, const DecodePlan& p, float* part,
                                    hipStream_t stream) {
   if constexpr (MT == 1) {  // 4- and 16-wave workgroups are planned for M <= 16 only
-    if (p.waves == 4) return launch_decode_w<MT, 4>(a, p, part, stream);
-    if (p.waves == 16) return launch_decode_w<MT, 16>(a, p, part, stream);
+    if (p.waves == 4) return launch_decode_w<MT, 4>(g, p, part, stream);
+    if (p.waves == 16) return launch_decode_w<MT, 16>(g, p, part, stream);
   }
-  return launch_decode_w<MT, 8>(a, p, part, stream);
+  return launch_decode_w<MT, 8>(g, p, part, stream);
+}
+
+static hipError_t launch_decode_any(const GroupArgs& g, const DecodePlan& p, float* part,
+                                    hipStream_t stream) {
+  if (p.reg) return launch_decode_reg(g, p, stream);
+  switch ((g.a[0].M + 15) / 16) {
+    case 1: return launch_decode_mt<1>(g, p, part, stream);
+    case 2: return launch_decode_mt<2>(g, p, part, stream);
+    case 3: return launch_decode_mt<3>(g, p, part, stream);
+    case 4: return launch_decode_mt<4>(g, p, part, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream) {
-  if (p.reg) return launch_decode_reg(a, p, stream);
-  switch ((a.M + 15) / 16) {
-    case 1: return launch_decode_mt<1>(a, p, part, stream);
-    case 2: return launch_decode_mt<2>(a, p, part, stream);
-    case 3: return launch_decode_mt<3>(a, p, part, stream);
-    case 4: return launch_decode_mt<4>(a, p, part, stream);
-    default: return hipErrorInvalidValue;
-  }
+  GroupArgs g{};
+  g.count = 1;
+  g.a[0] = a;
+  return launch_decode_any(g, p, part, stream);
+}
+
+hipError_t launch_decode_group(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
+  if (g.count < 1 || g.count > kGroupMax || p.splits != 1) return hipErrorInvalidValue;
+  return launch_decode_any(g, p, nullptr, stream);
 }
 
 template <int MT2, int S, int PB, int GPC, bool ACT>
@@ -1486,6 +1598,78 @@ hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t
   const size_t total = (size_t)K * N / 32;
   dequant_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
       (const u4*)pq, pz, ps, perm, w, ldw, K, N, gs, G);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Decoder-stage helpers around the GEMM (reference: cuda_extends/exllama/
+// fuse_v2/rms_norm.cu and q_mlp.cu silu_mul_kernel, restated).
+// ---------------------------------------------------------------------------
+
+// h = fp16(silu(g) * u), one element per thread; h may be g itself.
+__global__ void silu_mul_kernel(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
+                                uint16_t* h, int64_t ldh, int m, int n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)m * n) return;
+  const int64_t r = i / n;
+  const int64_t c = i - r * n;
+  const float gv = (float)as_h(g[r * ldg + c]);
+  const float uv = (float)as_h(u[r * ldu + c]);
+  h[r * ldh + c] = h_bits((_Float16)(silu_f32(gv) * uv));
+}
+
+hipError_t launch_silu_mul(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
+                           uint16_t* h, int64_t ldh, int m, int n, hipStream_t stream) {
+  const int64_t total = (int64_t)m * n;
+  silu_mul_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(g, ldg, u, ldu, h, ldh, m, n);
+  return hipGetLastError();
+}
+
+// One 256-thread workgroup per row: fp32 sum of squares of the row (inputs
+// clamped to the finite fp16 range, as the reference does), each thread over
+// its 8-element units, then a fixed butterfly within each wave and a fixed
+// order across the four waves; r = 1 / sqrt(sum / k + eps);
+// y = fp16((x * w) * r).  k % 8 == 0, rows 16-byte aligned.
+__global__ void __launch_bounds__(256)
+rms_norm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
+                float eps, uint16_t* __restrict__ y, int64_t ldy, int k) {
+  __shared__ float wsum[4];
+  const int tid = threadIdx.x;
+  const h8* xr = reinterpret_cast<const h8*>(x + (size_t)blockIdx.x * ldx);
+  const h8* wr = reinterpret_cast<const h8*>(w);
+  h8* yr = reinterpret_cast<h8*>(y + (size_t)blockIdx.x * ldy);
+  const int units = k / 8;
+  float sum = 0.f;
+  for (int u = tid; u < units; u += 256) {
+    const h8 v = xr[u];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = fmaxf(-65504.0f, fminf((float)v[e], 65504.0f));
+      sum = fmaf(f, f, sum);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if ((tid & 63) == 0) wsum[tid >> 6] = sum;
+  __syncthreads();
+  const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+  const float r = 1.0f / sqrtf(total / (float)k + eps);
+  for (int u = tid; u < units; u += 256) {
+    const h8 v = xr[u];
+    const h8 wv = wr[u];
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = fmaxf(-65504.0f, fminf((float)v[e], 65504.0f));
+      o[e] = (_Float16)(f * (float)wv[e] * r);
+    }
+    yr[u] = o;
+  }
+}
+
+hipError_t launch_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                           uint16_t* y, int64_t ldy, int m, int k, hipStream_t stream) {
+  rms_norm_kernel<<<(unsigned)m, 256, 0, stream>>>(x, ldx, w, eps, y, ldy, k);
   return hipGetLastError();
 }
 

@@ -27,10 +27,22 @@ DW4_PATH_AUTO = 0
 DW4_PATH_DECODE = 1
 DW4_PATH_PREFILL = 2
 
-# Every symbol the public header declares, with its ctypes signature.
 _c = ctypes
 _P = _c.c_void_p
 _SZ = _c.POINTER(_c.c_size_t)
+
+
+class Item(ctypes.Structure):
+    """``dw4_item``: one quantized matrix (packed buffers) and its output."""
+
+    _fields_ = [("k", _c.c_int), ("n", _c.c_int), ("group_size", _c.c_int),
+                ("packed_qweight", _P), ("packed_zeros", _P), ("packed_scales", _P),
+                ("perm", _P), ("bias", _P), ("y", _P), ("ldy", _c.c_int64)]
+
+
+_IP = _c.POINTER(Item)
+
+# Every symbol the public header declares, with its ctypes signature.
 SIGNATURES = {
     "dw4_abi_version": (_c.c_int, []),
     "dw4_strerror": (_c.c_char_p, [_c.c_int]),
@@ -46,8 +58,17 @@ SIGNATURES = {
                                  _P, _c.c_size_t, _P]),
     "dw4_dequant": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
                                _c.c_int64, _P]),
+    "dw4_gemm_group": (_c.c_int, [_c.c_int, _IP, _c.c_int, _P, _c.c_int64, _P, _c.c_size_t, _P]),
+    "dw4_gemm_silu_mul": (_c.c_int, [_c.c_int, _P, _c.c_int64, _IP, _IP, _P, _c.c_int64,
+                                     _P, _c.c_size_t, _P]),
+    "dw4_rms_norm": (_c.c_int, [_c.c_int, _c.c_int, _P, _c.c_int64, _P, _c.c_float, _P,
+                                _c.c_int64, _P]),
+    "dw4_attention_qkv_stage": (_c.c_int, [_c.c_int, _P, _c.c_int64, _P, _c.c_float, _P,
+                                           _c.c_int64, _IP, _IP, _IP, _P, _c.c_size_t, _P]),
+    "dw4_mlp_forward": (_c.c_int, [_c.c_int, _P, _c.c_int64, _P, _c.c_float, _P, _c.c_int64,
+                                   _IP, _IP, _IP, _P, _c.c_size_t, _P]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

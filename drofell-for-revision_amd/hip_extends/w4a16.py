@@ -11,7 +11,11 @@ relative to ``/root/reference/After-Revision-DROFELL``):
   ``__init__``, ``matmul`` with M-based dispatch, dequantised-weight
   export, transposed product for the PEFT backward);
 * :class:`Q4LinearFunction` / :class:`Q4ForwardOnlyLinearFunction` --
-  ``exllama.py:649-696,730-740``.
+  ``exllama.py:649-696,730-740``;
+* :func:`attention_forward_qkv_stage_v2_py` / :func:`mlp_forward_v2_py` --
+  the fused decoder-stage calls ``exllama.py:120-130`` (RMSNorm, then the
+  q/k/v projections as one grouped launch; RMSNorm, gate/up with the
+  silu * mul folded into one launch, then down).
 
 All device work goes through ``libdrofell_w4a16.so``; there is no CPU or
 PyTorch fallback for the forward product.
@@ -19,8 +23,11 @@ PyTorch fallback for the forward product.
 from __future__ import annotations
 
 import ctypes
+import hashlib
+import threading
+import weakref
 from dataclasses import dataclass
-from typing import Any, Optional, Tuple
+from typing import Any, Dict, Optional, Tuple
 
 import torch
 from torch.autograd import Function
@@ -108,6 +115,26 @@ def _aligned_rows(x2: torch.Tensor) -> torch.Tensor:
     return x2
 
 
+# Device perms by content: matrices whose act-order permutations are equal
+# (q/k/v, or gate/up, quantised against the same input) share one tensor, so
+# a fused launch can pair them.
+_perm_lock = threading.Lock()
+_perm_intern: Dict[Tuple[str, int, str], Tuple[torch.Tensor, "weakref.ref[torch.Tensor]"]] = {}
+
+
+def _shared_perm(perm_host: torch.Tensor, device: torch.device) -> torch.Tensor:
+    key = (str(device), perm_host.numel(), hashlib.sha1(perm_host.numpy().tobytes()).hexdigest())
+    with _perm_lock:
+        hit = _perm_intern.get(key)
+        if hit is not None:
+            dev = hit[1]()
+            if dev is not None and torch.equal(hit[0], perm_host):
+                return dev
+        dev = perm_host.to(device)
+        _perm_intern[key] = (perm_host.clone(), weakref.ref(dev))
+        return dev
+
+
 class Q4MatrixV2(object):
     """One repacked GPTQ projection on a HIP device.
 
@@ -154,7 +181,7 @@ class Q4MatrixV2(object):
                       perm_host.data_ptr())
             # g_idx == k // group_size sorts to the identity: no gather needed
             if not torch.equal(perm_host, torch.arange(height, dtype=torch.int32)):
-                perm = perm_host.to(self.device)
+                perm = _shared_perm(perm_host, self.device)
         self.use_act = perm is not None
         self.perm: torch.Tensor = perm if perm is not None else \
             torch.empty(0, dtype=torch.int32, device=self.device)
@@ -173,6 +200,12 @@ class Q4MatrixV2(object):
         cache.update_workspace_size(sizes["workspace"])
         cache.update_temp_weight_size(height * width)
         self.reconstructed_weight_float16: Optional[torch.Tensor] = None
+
+    @property
+    def cuda_q4(self) -> "Q4MatrixV2":
+        """The handle the fused stage calls take (the reference's ``make_q4``
+        pointer, ``exllama.py:203``): the matrix object itself."""
+        return self
 
     # -- configuration -------------------------------------------------------
     def set_tuning_params(self, tuning_params: TuningParams) -> None:
@@ -342,3 +375,135 @@ class Q4ForwardOnlyLinearFunction(Function):
     @staticmethod
     def backward(ctx: Any, grad_output: torch.Tensor):  # type: ignore[override]
         return None, None, None
+
+
+# ---------------------------------------------------------------------------
+# Decoder-stage calls
+# ---------------------------------------------------------------------------
+def _item(q4: Q4MatrixV2, y: Optional[torch.Tensor]) -> _lib.Item:
+    return _lib.Item(q4.height, q4.width, q4.group_size, q4.qweight.data_ptr(),
+                     q4.qzeros.data_ptr(), q4.scales.data_ptr(),
+                     q4.perm.data_ptr() if q4.use_act else None, None,
+                     None if y is None else y.data_ptr(), 0 if y is None else y.stride(0))
+
+
+def _rows(t: torch.Tensor, m: int, width: int, what: str) -> torch.Tensor:
+    """The first m rows of t viewed as fp16 [*, width] (row-major storage)."""
+    if t.dtype != torch.float16:
+        raise TypeError(f"{what} must be float16, got {t.dtype}")
+    v = t.view(-1, width)
+    if v.shape[0] < m:
+        raise ValueError(f"{what} holds {v.shape[0]} rows of {width}, need {m}")
+    return v[:m]
+
+
+def _matrix(h: Any) -> Q4MatrixV2:
+    q4 = getattr(h, "cuda_q4", h)
+    if not isinstance(q4, Q4MatrixV2):
+        raise TypeError(f"expected a Q4MatrixV2 handle, got {type(h).__name__}")
+    return q4
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``fp16(x * w / sqrt(mean(x^2) + eps))`` per row of fp16 x [..., K]
+    (the reference's ``rms_norm_cuda``, ``fuse_v2/rms_norm.cu:26-131``)."""
+    k = x.shape[-1]
+    x2 = _aligned_rows(x.reshape(-1, k))
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    o2 = _rows(out, m, k, "out")
+    w = weight.to(torch.float16).contiguous()
+    _lib.check("dw4_rms_norm", _lib.load().dw4_rms_norm(
+        m, k, x2.data_ptr(), x2.stride(0), w.data_ptr(), float(eps), o2.data_ptr(), o2.stride(0),
+        _stream(x.device)))
+    return out
+
+
+def attention_forward_qkv_stage_v2_py(layernorm: torch.Tensor, norm_epsilon: float,
+                                      q_proj: Any, k_proj: Any, v_proj: Any,
+                                      temp_rms_output: torch.Tensor, temp_q_output: torch.Tensor,
+                                      temp_k_output: torch.Tensor, temp_v_output: torch.Tensor,
+                                      temp_weight: Optional[torch.Tensor], x: torch.Tensor,
+                                      BLOCK_KN_SIZE: int, BLOCK_M_SIZE_MAX: int,
+                                      MATMAL_RECONSTRUCT_THRESHOLD_V2: int,
+                                      q_len: int, batch_size: int) -> None:
+    """``temp_rms_output = rms_norm(x)``; ``temp_{q,k,v}_output = rms @ W``.
+
+    Same arguments as the reference (``exllama.py:124-130`` ->
+    ``fuse_v2/q_attn.cu:23-54``).  The q/k/v products run as one grouped
+    launch where the decode kernel applies.  ``temp_weight`` and the three
+    exllama tuning values are accepted and unused: this library chooses its
+    kernels from M and the shapes.
+    """
+    q4s = [_matrix(h) for h in (q_proj, k_proj, v_proj)]
+    hidden = q4s[0].height
+    m = q_len * batch_size
+    x2 = _aligned_rows(_rows(x, m, hidden, "x"))
+    rms = _rows(temp_rms_output, m, hidden, "temp_rms_output")
+    outs = [_rows(t, m, q4.width, name) for t, q4, name in
+            ((temp_q_output, q4s[0], "temp_q_output"), (temp_k_output, q4s[1], "temp_k_output"),
+             (temp_v_output, q4s[2], "temp_v_output"))]
+    items = [_item(q4, y) for q4, y in zip(q4s, outs)]
+    ws = q4s[0].cache.workspace
+    w = layernorm.to(torch.float16).contiguous()
+    _lib.check("dw4_attention_qkv_stage", _lib.load().dw4_attention_qkv_stage(
+        m, x2.data_ptr(), x2.stride(0), w.data_ptr(), float(norm_epsilon),
+        rms.data_ptr(), rms.stride(0), ctypes.byref(items[0]), ctypes.byref(items[1]),
+        ctypes.byref(items[2]), ws.data_ptr(), ws.numel(), _stream(x.device)))
+
+
+def mlp_forward_v2_py(layernorm: torch.Tensor, norm_epsilon: float, gate_q4: Any, up_q4: Any,
+                      down_q4: Any, temp_rms_output: torch.Tensor,
+                      temp_gate_output: torch.Tensor, temp_up_output: torch.Tensor,
+                      temp_weight: Optional[torch.Tensor], x: torch.Tensor,
+                      output: torch.Tensor, BLOCK_KN_SIZE: int, BLOCK_M_SIZE_MAX: int,
+                      MATMAL_RECONSTRUCT_THRESHOLD_V2: int) -> None:
+    """``output = (silu(rms @ W_gate) * (rms @ W_up)) @ W_down`` with
+    ``rms = rms_norm(x)``.
+
+    Same arguments as the reference (``exllama.py:120-121`` ->
+    ``fuse_v2/q_mlp.cu:96-133``): ``temp_rms_output`` receives the
+    normalised input and ``temp_gate_output`` the gated product that feeds
+    down; ``temp_up_output`` is scratch.  For small M (decode) gate and up
+    run as one launch that never writes their separate products.
+    ``temp_weight`` and the tuning values are accepted and unused.
+    """
+    g, u, d = _matrix(gate_q4), _matrix(up_q4), _matrix(down_q4)
+    hidden = g.height
+    x2 = _aligned_rows(x.reshape(-1, hidden))
+    m = x2.shape[0]
+    rms = _rows(temp_rms_output, m, hidden, "temp_rms_output")
+    hbuf = _rows(temp_gate_output, m, g.width, "temp_gate_output")
+    ubuf = _rows(temp_up_output, m, u.width, "temp_up_output")
+    out = _rows(output, m, d.width, "output")
+    ig, iu, idn = _item(g, hbuf), _item(u, ubuf), _item(d, out)
+    ws = g.cache.workspace
+    w = layernorm.to(torch.float16).contiguous()
+    _lib.check("dw4_mlp_forward", _lib.load().dw4_mlp_forward(
+        m, x2.data_ptr(), x2.stride(0), w.data_ptr(), float(norm_epsilon),
+        rms.data_ptr(), rms.stride(0), ctypes.byref(ig), ctypes.byref(iu), ctypes.byref(idn),
+        ws.data_ptr(), ws.numel(), _stream(x.device)))
+
+
+def gemm_group(x: torch.Tensor, matrices: "list[Q4MatrixV2]",
+               outputs: Optional["list[Optional[torch.Tensor]]"] = None) -> "list[torch.Tensor]":
+    """``[x @ W_i]`` for matrices that share x (one launch where the decode
+    kernel applies); fp16 x [..., K]."""
+    q4s = [_matrix(h) for h in matrices]
+    k = q4s[0].height
+    x2 = _aligned_rows(x.reshape(-1, k))
+    m = x2.shape[0]
+    outs = []
+    for i, q4 in enumerate(q4s):
+        o = outputs[i] if outputs is not None and outputs[i] is not None else \
+            torch.empty(x.shape[:-1] + (q4.width,), dtype=torch.float16, device=x.device)
+        outs.append(o)
+    items = (_lib.Item * len(q4s))(*[_item(q4, _rows(o, m, q4.width, "output"))
+                                     for q4, o in zip(q4s, outs)])
+    ws = q4s[0].cache.workspace
+    _lib.check("dw4_gemm_group", _lib.load().dw4_gemm_group(
+        len(q4s), items, m, x2.data_ptr(), x2.stride(0), ws.data_ptr(), ws.numel(),
+        _stream(x.device)))
+    return outs

@@ -16,6 +16,15 @@
  *                    Q4MatrixV2.matmul (cuda_extends/exllama.py:492-526)
  *   dw4_dequant      q4_to_half_matrix_v2 (entry.cpp:79-91) and
  *                    marlin_dequant_into (cuda_extends/marlin/marlin_dequant.cu:97-172)
+ *   dw4_gemm_group   the q/k/v GEMMs of attention_forward_qkv_stage
+ *                    (cuda_extends/exllama/fuse_v2/q_attn.cu:46-48) and the
+ *                    gate/up GEMMs of mlp_forward (fuse_v2/q_mlp.cu:119-120)
+ *   dw4_gemm_silu_mul  gate/up GEMMs + silu_mul_kernel of mlp_forward
+ *                    (fuse_v2/q_mlp.cu:119-130, silu_mul_kernel :44-85)
+ *   dw4_rms_norm     rms_norm_cuda (fuse_v2/rms_norm.cu:26-93, 109-131)
+ *   dw4_attention_qkv_stage  attention_forward_qkv_stage_v2
+ *                    (entry.cpp:483-532 -> fuse_v2/q_attn.cu:23-54)
+ *   dw4_mlp_forward  mlp_forward_v2 (entry.cpp:431-481 -> fuse_v2/q_mlp.cu:96-133)
  *
  * Conventions
  *   - Every function returns an int status (DW4_OK == 0); no exception or
@@ -73,7 +82,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 1
+#define DW4_ABI_VERSION 2
 
 enum {
   DW4_OK = 0,
@@ -146,6 +155,65 @@ int dw4_dequant(int k, int n, int group_size,
                 const int32_t* packed_qweight, const int32_t* packed_zeros,
                 const uint16_t* packed_scales, const int32_t* perm,
                 uint16_t* w, int64_t ldw, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Decoder-stage calls: several projections of one layer per launch.
+ * ------------------------------------------------------------------------- */
+
+/* One quantized matrix (buffers from dw4_repack for k, n, group_size, perm
+ * as given to dw4_repack) and its output y fp16 [m, n], row stride ldy.
+ * bias: NULL or fp16 [n]. */
+typedef struct dw4_item {
+  int k, n, group_size;
+  const int32_t* packed_qweight;
+  const int32_t* packed_zeros;
+  const uint16_t* packed_scales;
+  const int32_t* perm;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t ldy;
+} dw4_item;
+
+/* y_i = x @ W_i (+ bias_i) for 1..4 matrices that share x, k and
+ * group_size (with perm on all or on none).  Where DW4_PATH_AUTO would take
+ * the decode kernel for the summed N, one launch covers every strip of every
+ * matrix; otherwise (and where that launch would split K) the matrices run
+ * one after another as dw4_gemm does.  workspace: at least
+ * dw4_workspace_size of each item. */
+int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, int64_t ldx,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* h = fp16(silu(g) * u) with g = fp16(x @ W_gate (+ bias)),
+ * u = fp16(x @ W_up (+ bias)), silu(v) = v / (1 + exp(-v)) in fp32.
+ * gate and up: equal k, n, group_size and the same perm pointer (or both
+ * NULL).  For m <= 32 where DW4_PATH_AUTO takes the decode kernel, one
+ * launch keeps both products in registers and gate->y, up->y are not
+ * written.  Otherwise the products are written to gate->y and up->y
+ * (required then) and an elementwise pass writes h; h may be gate->y with
+ * ldh == gate->ldy. */
+int dw4_gemm_silu_mul(int m, const uint16_t* x, int64_t ldx, const dw4_item* gate,
+                      const dw4_item* up, uint16_t* h, int64_t ldh, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* y = fp16(x * w * 1/sqrt(mean(x^2) + eps)) for each row of x fp16 [m, k]
+ * (w fp16 [k]; fp32 sums in a fixed order).  k % 8 == 0; x, w, y 16-byte
+ * aligned; ldx, ldy multiples of 8; y must not overlap x. */
+int dw4_rms_norm(int m, int k, const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
+                 uint16_t* y, int64_t ldy, void* stream);
+
+/* rms = rms_norm(x, norm_w, eps) (fp16 [m, k], row stride ldr), then
+ * q, k, v = rms @ W (dw4_gemm_group of the three items). */
+int dw4_attention_qkv_stage(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w,
+                            float eps, uint16_t* rms, int64_t ldr, const dw4_item* q,
+                            const dw4_item* k, const dw4_item* v, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* rms = rms_norm(x, norm_w, eps); h = silu(rms @ W_gate) * (rms @ W_up)
+ * written to gate->y (dw4_gemm_silu_mul with h = gate->y; up->y is the
+ * second temporary); down->y = h @ W_down.  down->k == gate->n. */
+int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
+                    uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+                    const dw4_item* down, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

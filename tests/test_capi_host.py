@@ -28,11 +28,11 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 9, names
+    assert len(names) == 14, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
-    assert lib.dw4_abi_version() == 1
+    assert lib.dw4_abi_version() == 2
 
 
 def test_strerror_names_every_status():
@@ -76,6 +76,42 @@ def test_shape_validation_codes():
                            None) == _lib.DW4_ERR_INVALID_ARG
     assert lib.dw4_gemm_path(7, 0, 1, 128, 64, 128, None, 128, None, None, None, None, None,
                              None, 64, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+
+
+def test_stage_entry_points_validate_before_launch():
+    lib = _lib.load()
+    fake = 1 << 20  # 16-byte aligned non-null address; never dereferenced on these paths
+
+    def item(k=4096, n=4096, g=128, perm=None, y=fake):
+        return _lib.Item(k, n, g, fake, fake, fake, perm, None, y, n)
+
+    two = (_lib.Item * 2)(item(), item(k=4224))
+    assert lib.dw4_gemm_group(2, two, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    one = (_lib.Item * 1)(item())
+    assert lib.dw4_gemm_group(0, one, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_gemm_group(5, one, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    mixed = (_lib.Item * 2)(item(), item(perm=fake))  # act-order on one matrix only
+    assert lib.dw4_gemm_group(2, mixed, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    noout = (_lib.Item * 1)(item(y=None))
+    assert lib.dw4_gemm_group(1, noout, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_gemm_group(1, one, 0, None, 4096, None, 0, None) == _lib.DW4_OK
+    odd = (_lib.Item * 1)(item(n=100))
+    assert lib.dw4_gemm_group(1, odd, 1, fake, 4096, None, 0, None) == _lib.DW4_ERR_UNSUPPORTED
+    g, u = item(n=11008), item(n=4096)
+    assert lib.dw4_gemm_silu_mul(1, fake, 4096, ctypes.byref(g), ctypes.byref(u), fake, 11008,
+                                 None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_gemm_silu_mul(1, fake, 4096, ctypes.byref(g), ctypes.byref(g), None, 11008,
+                                 None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_rms_norm(1, 4100, fake, 4104, fake, 1e-5, fake, 4104,
+                            None) == _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_rms_norm(1, 4096, fake + 2, 4096, fake, 1e-5, fake, 4096,
+                            None) == _lib.DW4_ERR_MISALIGNED
+    assert lib.dw4_rms_norm(1, 4096, fake, 4096, fake, -1.0, fake, 4096,
+                            None) == _lib.DW4_ERR_INVALID_ARG
+    down = item(k=4096, n=4096)  # down->k must equal gate->n (11008)
+    assert lib.dw4_mlp_forward(1, fake, 4096, fake, 1e-5, fake, 4096, ctypes.byref(g),
+                               ctypes.byref(g), ctypes.byref(down), None, 0,
+                               None) == _lib.DW4_ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("k,g", [(256, 32), (4096, 128), (13824, 128)])

@@ -395,3 +395,140 @@ def test_invariance_catches_wrong_group_lookup():
     good = gptq.gemm_ref(x, gptq.dequantize(qw, qz, s, g_idx))
     wrong = gptq.gemm_ref(x, gptq.dequantize(qw, qz, s, (np.arange(K) // g).astype(np.int32)))
     assert not np.allclose(good, wrong, rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# decoder-stage operations (oracle/stage.py)
+# ---------------------------------------------------------------------------
+from oracle import stage  # noqa: E402
+
+
+def _rms_checks(fn) -> list:
+    """Failures of an rms_norm candidate against what the mathematics fixes."""
+    bad = []
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal(64) * 0.5 + 1).astype(np.float16)
+    # constant positive row, eps = 0: x / rms(x) == 1 exactly, so y == w
+    if not np.array_equal(fn(np.full((1, 64), 3.0, np.float16), w, 0.0)[0].view(np.uint16),
+                          w.view(np.uint16)):
+        bad.append("constant row")
+    # eps = 0 and w = 1: the output has mean square 1 (up to fp16 rounding)
+    x = rng.standard_normal((3, 64)).astype(np.float16)
+    y = fn(x, np.ones(64, np.float16), 0.0).astype(np.float64)
+    if not np.allclose((y * y).mean(axis=1), 1.0, atol=3e-3):
+        bad.append("unit mean square")
+    # exact power-of-two scaling of x leaves y unchanged when eps = 0
+    if not np.array_equal(fn(x, w, 0.0).view(np.uint16), fn(x * np.float16(4), w, 0.0).view(np.uint16)):
+        bad.append("scale invariance")
+    # eps dominates a tiny row: y ~= x * w / sqrt(eps)
+    tiny = np.full((1, 64), 1e-3, np.float16)
+    expect = (tiny.astype(np.float64) * w.astype(np.float64) / np.sqrt(1.0 + 1e-6)).astype(np.float16)
+    if np.max(np.abs(fn(tiny, w, 1.0).astype(np.float64) - expect.astype(np.float64))) > 1e-6:
+        bad.append("eps term")
+    return bad
+
+
+def test_rms_norm_pinned():
+    assert _rms_checks(stage.rms_norm) == []
+    # an independent library routine in float64, rounded once to fp16
+    import torch
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((4, 4096)) * 3).astype(np.float16)
+    w = (rng.standard_normal(4096) * 0.1 + 1).astype(np.float16)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (4096,),
+                                       torch.from_numpy(w).double(), 1e-5).half().numpy()
+    got = stage.rms_norm(x, w, 1e-5)
+    ulps = np.abs(got.view(np.uint16).astype(np.int32) - ref.view(np.uint16).astype(np.int32))
+    assert ulps.max() <= 1 and (ulps == 0).mean() > 0.99
+
+
+@pytest.mark.parametrize("name", ["sum", "eps_outside", "no_weight"])
+def test_rms_checks_catch_planted_mistakes(name):
+    def mutant(x, w, eps):
+        xf = np.asarray(x, np.float16).astype(np.float64)
+        wf = np.asarray(w, np.float16).astype(np.float64)
+        ss = (xf * xf).sum(axis=-1, keepdims=True)
+        if name == "sum":
+            r = 1.0 / np.sqrt(ss + eps)                     # sum, not mean
+        elif name == "eps_outside":
+            r = 1.0 / (np.sqrt(ss / xf.shape[-1]) + eps)    # eps added after the root
+        else:
+            r = 1.0 / np.sqrt(ss / xf.shape[-1] + eps)
+            wf = np.ones_like(wf)                           # weight dropped
+        return (xf * wf * r).astype(np.float16)
+    assert _rms_checks(mutant) != []
+
+
+def _silu_checks(fn) -> list:
+    bad = []
+    half = lambda v: np.asarray(v, np.float16)  # noqa: E731
+    one = half([1.0])
+    if fn(half([0.0]), one)[0] != 0:
+        bad.append("silu(0)")
+    ln3 = float(np.float16(np.log(3.0)))
+    sig = 1.0 / (1.0 + np.exp(-ln3))  # = 3/4 only at exactly ln 3; use the fp16 input
+    if fn(half([ln3]), one)[0] != np.float16(ln3 * sig):
+        bad.append("silu(ln 3)")
+    # silu(v) - silu(-v) = v
+    v = np.linspace(-8, 8, 33).astype(np.float16)
+    d = fn(v, np.ones_like(v)).astype(np.float64) - fn(-v, np.ones_like(v)).astype(np.float64)
+    if np.max(np.abs(d - v.astype(np.float64))) > 2e-2:
+        bad.append("odd part")
+    # u scales linearly; g is the gated input
+    g = half([1.5, -2.0, 3.0])
+    u = half([2.0, 0.5, -1.0])
+    from scipy.special import expit
+    ref = (g.astype(np.float64) * expit(g.astype(np.float64)) * u.astype(np.float64)).astype(np.float16)
+    if not np.array_equal(fn(g, u).view(np.uint16), ref.view(np.uint16)):
+        bad.append("library sigmoid")
+    return bad
+
+
+def test_silu_mul_pinned():
+    assert _silu_checks(stage.silu_mul) == []
+    from scipy.special import expit
+    rng = np.random.default_rng(7)
+    g = (rng.standard_normal(4096) * 4).astype(np.float16)
+    u = rng.standard_normal(4096).astype(np.float16)
+    ref = (g.astype(np.float64) * expit(g.astype(np.float64)) * u.astype(np.float64)).astype(np.float16)
+    assert np.array_equal(stage.silu_mul(g, u).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("name", ["swapped", "sigmoid", "gelu"])
+def test_silu_checks_catch_planted_mistakes(name):
+    def mutant(g, u):
+        gf = np.asarray(g, np.float16).astype(np.float64)
+        uf = np.asarray(u, np.float16).astype(np.float64)
+        if name == "swapped":
+            return (stage.silu(uf) * gf).astype(np.float16)
+        if name == "sigmoid":
+            return (1.0 / (1.0 + np.exp(-gf)) * uf).astype(np.float16)
+        return (0.5 * gf * (1 + np.tanh(0.7978845608 * (gf + 0.044715 * gf ** 3))) * uf).astype(np.float16)
+    assert _silu_checks(mutant) != []
+
+
+def _identity_layer(k: int, scale: float):
+    """GPTQ buffers whose dequantised weight is scale * I (k x k)."""
+    q = np.full((k, k), 7, dtype=np.uint8)
+    q[np.arange(k), np.arange(k)] = 8       # q - z_eff = 1 on the diagonal
+    z = np.full((1, k), 6, dtype=np.uint8)  # effective zero 7
+    s = np.full((1, k), scale, dtype=np.float16)
+    g_idx = np.zeros(k, dtype=np.int32)
+    return gptq.dequantize(gptq.pack_qweight(q), gptq.pack_qzeros(z), s, g_idx)
+
+
+def test_stage_composition_on_identity_weights():
+    k = 64
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, k)).astype(np.float16)
+    nw = (rng.standard_normal(k) * 0.2 + 1).astype(np.float16)
+    eye, two = _identity_layer(k, 1.0), _identity_layer(k, 2.0)
+    assert np.array_equal(eye, np.eye(k, dtype=np.float16))
+    rms, (q, kk, v) = stage.qkv_stage(x, nw, 1e-5, [eye, two, eye])
+    assert np.array_equal(q.astype(np.float16), rms) and np.array_equal(kk, 2 * rms.astype(np.float64))
+    rms2, h, out = stage.mlp_forward(x, nw, 1e-5, eye, two, eye)
+    r = rms2.astype(np.float64)
+    # gate = rms, up = 2 rms: h = silu(rms) * 2 rms (a swapped pair gives silu(2 rms) * rms)
+    from scipy.special import expit
+    assert np.array_equal(h.view(np.uint16), (r * expit(r) * 2 * r).astype(np.float16).view(np.uint16))
+    assert np.array_equal(out.astype(np.float16), h)
