@@ -314,6 +314,17 @@ int gemm_item(int m, const uint16_t* x, int64_t ldx, const dw4_item* it, void* w
                        it->y, it->ldy, ws, wsb, stream);
 }
 
+
+int check_pair(const dw4_item* gate, const dw4_item* up) {
+  int st = check_item(gate);
+  if (st == DW4_OK) st = check_item(up);
+  if (st != DW4_OK) return st;
+  if (gate->k != up->k || gate->n != up->n || gate->group_size != up->group_size ||
+      (gate->perm == nullptr) != (up->perm == nullptr))
+    return DW4_ERR_INVALID_ARG;
+  return DW4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -419,6 +430,39 @@ int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_
                            stream);
   if (st != DW4_OK) return st;
   return gemm_item(m, gate->y, gate->ldy, down, workspace, workspace_bytes, stream);
+}
+
+int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint16_t* residual,
+                            int64_t ldres, const dw4_item* o, const uint16_t* norm_w, float eps,
+                            uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+                            const dw4_item* down, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (o == nullptr || gate == nullptr || up == nullptr || down == nullptr || residual == nullptr)
+    return DW4_ERR_INVALID_ARG;
+  int st = check_item(o);
+  if (st == DW4_OK) st = check_output(o);
+  if (st == DW4_OK) st = check_item(down);
+  if (st == DW4_OK) st = check_output(down);
+  if (st == DW4_OK) st = check_output(gate);
+  if (st == DW4_OK) st = check_pair(gate, up);
+  if (st != DW4_OK) return st;
+  if (ldres < o->n || o->n != gate->k || down->n != o->n || down->k != gate->n || m < 0)
+    return DW4_ERR_INVALID_ARG;
+  if (!(eps >= 0.0f) || norm_w == nullptr || rms == nullptr) return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  st = check_x(attn, lda, o->k);
+  if (st != DW4_OK) return st;
+  // o_proj, + residual, mlp_forward, + residual (real_fuse.py:80-103)
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = gemm_item(m, attn, lda, o, workspace, workspace_bytes, stream);
+  if (st == DW4_OK)
+    st = status_of(dw4::launch_add(residual, ldres, o->y, o->ldy, o->y, o->ldy, m, o->n, s));
+  if (st == DW4_OK)
+    st = dw4_mlp_forward(m, o->y, o->ldy, norm_w, eps, rms, ldr, gate, up, down, workspace,
+                         workspace_bytes, stream);
+  if (st != DW4_OK) return st;
+  return status_of(dw4::launch_add(o->y, o->ldy, down->y, down->ldy, down->y, down->ldy, m,
+                                   down->n, s));
 }
 
 }  // extern "C"

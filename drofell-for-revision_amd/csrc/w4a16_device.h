@@ -1,0 +1,94 @@
+// Device-side helpers shared by the gfx950 kernel files (types, the int4 ->
+// fp16 dequantisation identity, MFMA wrappers, activation gathers).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "w4a16_internal.h"
+
+namespace dw4 {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef int32_t i4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kMagic = 0x64006400u;  // fp16 1024.0 in both halves
+
+__device__ __forceinline__ h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+__device__ __forceinline__ _Float16 as_h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
+__device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ h2 splat2(_Float16 v) { return h2{v, v}; }
+
+// (a & mask) | magic in one VALU instruction.  Written out because the
+// compiler splits it into two when both constants are literals (a gfx9 VOP3
+// instruction cannot encode two literals); here the mask comes from an SGPR
+// and the magic value from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
+  return r;
+}
+
+// The 8 rows of one packed word, minus the effective zero, as exact fp16
+// integers in row order.  Even rows sit in the low half-word, odd rows in
+// the high half-word, so OR-ing a nibble pair into the fp16 pattern of
+// 1024.0 yields (1024 + q) or (1024 + 16 q) in each half without a shift.
+__device__ __forceinline__ h8 centered8(uint32_t w, h2 nz1024, h2 nz64, uint32_t magic) {
+  const h2 sixteenth = splat2((_Float16)0.0625f);
+  const uint32_t w8 = w >> 8;
+  const h2 p0 = as_h2(and_or(w, 0x000F000Fu, magic)) + nz1024;               // rows 0,1
+  const h2 p1 = as_h2(and_or(w, 0x00F000F0u, magic)) * sixteenth + nz64;     // rows 2,3
+  const h2 p2 = as_h2(and_or(w8, 0x000F000Fu, magic)) + nz1024;              // rows 4,5
+  const h2 p3 = as_h2(and_or(w8, 0x00F000F0u, magic)) * sixteenth + nz64;    // rows 6,7
+  const h4 a = __builtin_shufflevector(p0, p1, 0, 1, 2, 3);
+  const h4 b = __builtin_shufflevector(p2, p3, 0, 1, 2, 3);
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Zero-point constants -(1024 + z_eff) and -(64 + z_eff) (z_eff = stored + 1,
+// 1..16) built from their fp16 bit patterns: 1024 + z has exponent 10 and
+// mantissa z, 64 + z has exponent 6 and mantissa 16 z.
+__device__ __forceinline__ void zero_consts(uint32_t zword, int zshift, h2& nz1024, h2& nz64) {
+  const uint32_t ze = ((zword >> zshift) & 15u) + 1u;
+  nz1024 = as_h2((0xE400u | ze) * 0x00010001u);
+  nz64 = as_h2((0xD400u | (ze << 4)) * 0x00010001u);
+}
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// One 16-byte unit (8 consecutive sorted rows) of an activation row,
+// gathered through perm for act-order checkpoints.
+template <bool ACT>
+__device__ __forceinline__ h8 load_x_unit(const _Float16* __restrict__ row,
+                                          const int32_t* __restrict__ perm, int k) {
+  if (ACT) {
+    const i4 p0 = *(const i4*)(perm + k);
+    const i4 p1 = *(const i4*)(perm + k + 4);
+    return h8{row[p0[0]], row[p0[1]], row[p0[2]], row[p0[3]],
+              row[p1[0]], row[p1[1]], row[p1[2]], row[p1[3]]};
+  }
+  return *(const h8*)(row + k);
+}
+
+// Entry i of a per-item array of a grouped launch (item index wave-uniform).
+template <typename T, int L>
+__device__ __forceinline__ T pick(const T (&v)[L], int i) {
+  static_assert(kGroupMax == 4 && L >= 4, "pick() selects among four items");
+  return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
+// Item that owns workgroup b (wg0 ascending).
+__device__ __forceinline__ int item_of(const Items& d, int b) {
+  return (d.count > 1 && b >= d.wg0[1]) + (d.count > 2 && b >= d.wg0[2]) +
+         (d.count > 3 && b >= d.wg0[3]);
+}
+
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
+
+}  // namespace dw4

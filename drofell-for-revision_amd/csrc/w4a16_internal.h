@@ -15,6 +15,7 @@ constexpr int kDecodeMaxM = 64;      // four 16-row MFMA tiles
 constexpr int kDecodeAutoMaxM = 24;        // DW4_PATH_AUTO picks decode up to this M,
 constexpr int kDecodeAutoMaxMNarrow = 32;  // and up to this M when strips <= CUs
 constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
+constexpr int kMetaWords = kMetaBytes / 4;
 #ifndef DW4_DECODE_UMAX
 #define DW4_DECODE_UMAX 4  // deepest weight ring (chunks in flight per wave)
 #endif
@@ -168,6 +169,10 @@ constexpr size_t kWsHeadBytes = kSplitCounters * sizeof(int);
 inline size_t split_ws_bytes(int splits, size_t plane_floats) {
   return splits > 1 ? kWsHeadBytes + (size_t)splits * plane_floats * sizeof(float) : 0;
 }
+
+// y = fp16(a + b) over [m, n] (row strides lda, ldb, ldy); y may alias a or b.
+hipError_t launch_add(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* y,
+                      int64_t ldy, int m, int n, hipStream_t stream);
 
 hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* ws,
                           hipStream_t stream);

@@ -67,8 +67,11 @@ SIGNATURES = {
                                            _c.c_int64, _IP, _IP, _IP, _P, _c.c_size_t, _P]),
     "dw4_mlp_forward": (_c.c_int, [_c.c_int, _P, _c.c_int64, _P, _c.c_float, _P, _c.c_int64,
                                    _IP, _IP, _IP, _P, _c.c_size_t, _P]),
+    "dw4_decoder_after_stage": (_c.c_int, [_c.c_int, _P, _c.c_int64, _P, _c.c_int64, _IP, _P,
+                                           _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
+                                           _c.c_size_t, _P]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

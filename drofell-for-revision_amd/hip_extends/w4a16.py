@@ -487,6 +487,43 @@ def mlp_forward_v2_py(layernorm: torch.Tensor, norm_epsilon: float, gate_q4: Any
         ws.data_ptr(), ws.numel(), _stream(x.device)))
 
 
+def decoder_after_stage_v2_py(o_q4: Any, gate_q4: Any, up_q4: Any, down_q4: Any,
+                              layernorm: torch.Tensor, norm_epsilon: float,
+                              attn_output: torch.Tensor, residual: torch.Tensor,
+                              temp_hidden_output: torch.Tensor, temp_rms_output: torch.Tensor,
+                              temp_gate_output: torch.Tensor, temp_up_output: torch.Tensor,
+                              output: torch.Tensor) -> None:
+    """The decoder layer after attention, as ``_fuse_forward_after_stage``
+    (``operators/core/decoder_wrap/real_fuse.py:77-103``) computes it:
+
+    * ``temp_hidden_output = residual + o_proj(attn_output)``;
+    * ``temp_rms_output = rms_norm(temp_hidden_output)``;
+    * ``temp_gate_output = silu(rms @ W_gate) * (rms @ W_up)``;
+    * ``output = temp_hidden_output + temp_gate_output @ W_down``.
+
+    Every sum is rounded to fp16 as the reference's fp16 tensors are.
+    ``temp_up_output`` is scratch for the up product where gate and up do not
+    run as one launch.
+    """
+    o, g, u, d = _matrix(o_q4), _matrix(gate_q4), _matrix(up_q4), _matrix(down_q4)
+    hidden = o.width
+    a2 = _aligned_rows(attn_output.reshape(-1, o.height))
+    m = a2.shape[0]
+    res = _rows(residual, m, hidden, "residual")
+    x2 = _rows(temp_hidden_output, m, hidden, "temp_hidden_output")
+    rms = _rows(temp_rms_output, m, hidden, "temp_rms_output")
+    hbuf = _rows(temp_gate_output, m, g.width, "temp_gate_output")
+    ubuf = _rows(temp_up_output, m, u.width, "temp_up_output")
+    out = _rows(output, m, d.width, "output")
+    io, ig, iu, idn = _item(o, x2), _item(g, hbuf), _item(u, ubuf), _item(d, out)
+    ws = o.cache.workspace
+    w = layernorm.to(torch.float16).contiguous()
+    _lib.check("dw4_decoder_after_stage", _lib.load().dw4_decoder_after_stage(
+        m, a2.data_ptr(), a2.stride(0), res.data_ptr(), res.stride(0), ctypes.byref(io),
+        w.data_ptr(), float(norm_epsilon), rms.data_ptr(), rms.stride(0), ctypes.byref(ig),
+        ctypes.byref(iu), ctypes.byref(idn), ws.data_ptr(), ws.numel(), _stream(attn_output.device)))
+
+
 def gemm_group(x: torch.Tensor, matrices: "list[Q4MatrixV2]",
                outputs: Optional["list[Optional[torch.Tensor]]"] = None) -> "list[torch.Tensor]":
     """``[x @ W_i]`` for matrices that share x (one launch where the decode

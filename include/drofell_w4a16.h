@@ -25,6 +25,9 @@
  *   dw4_attention_qkv_stage  attention_forward_qkv_stage_v2
  *                    (entry.cpp:483-532 -> fuse_v2/q_attn.cu:23-54)
  *   dw4_mlp_forward  mlp_forward_v2 (entry.cpp:431-481 -> fuse_v2/q_mlp.cu:96-133)
+ *   dw4_decoder_after_stage  the o_proj, residual add, mlp_forward_v2 and
+ *                    residual add of DecoderWrapFuse._fuse_forward_after_stage
+ *                    (operators/core/decoder_wrap/real_fuse.py:77-103)
  *
  * Conventions
  *   - Every function returns an int status (DW4_OK == 0); no exception or
@@ -82,7 +85,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 2
+#define DW4_ABI_VERSION 3
 
 enum {
   DW4_OK = 0,
@@ -214,6 +217,20 @@ int dw4_attention_qkv_stage(int m, const uint16_t* x, int64_t ldx, const uint16_
 int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
                     uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
                     const dw4_item* down, void* workspace, size_t workspace_bytes, void* stream);
+
+/* x2 = fp16(residual + fp16(attn @ W_o (+ bias)))          -> o->y
+ * rms = rms_norm(x2, norm_w, eps)                            -> rms
+ * h = fp16(silu(rms @ W_gate) * (rms @ W_up))               -> gate->y
+ * out = fp16(x2 + fp16(h @ W_down (+ bias)))                 -> down->y
+ * attn fp16 [m, o->k] (row stride lda), residual fp16 [m, o->n] (ldres).
+ * o->n == gate->k == down->n, down->k == gate->n.  up->y receives the up
+ * product where gate and up cannot run as one launch (as dw4_gemm_silu_mul).
+ * Runs as o_proj, an fp16 add, dw4_mlp_forward and an fp16 add. */
+int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint16_t* residual,
+                            int64_t ldres, const dw4_item* o, const uint16_t* norm_w, float eps,
+                            uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+                            const dw4_item* down, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 #ifdef __cplusplus
 }

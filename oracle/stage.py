@@ -18,7 +18,10 @@ to ``/root/reference/After-Revision-DROFELL``):
   (``attention_forward_qkv_stage``: rms_norm, then q, k, v from the
   normalised fp16 rows);
 * ``mlp_forward`` -- ``fuse_v2/q_mlp.cu:96-133`` (rms_norm, gate and up
-  from the normalised rows, each rounded to fp16, silu_mul, then down).
+  from the normalised rows, each rounded to fp16, silu_mul, then down);
+* ``after_stage`` -- ``operators/core/decoder_wrap/real_fuse.py:77-103``
+  (``_fuse_forward_after_stage``: o_proj, ``residual + o`` in fp16,
+  mlp_forward on that sum, then ``sum + mlp`` in fp16).
 
 The reference evaluates silu in fp16 arithmetic with CUDA's half-precision
 exp and reciprocal; this restatement (and the HIP kernels) evaluate it
@@ -75,3 +78,22 @@ def mlp_forward(x: np.ndarray, norm_w: np.ndarray, eps: float, w_gate: np.ndarra
     u = gptq.gemm_ref(rms, w_up).astype(np.float16)
     h = silu_mul(g, u)
     return rms, h, gptq.gemm_ref(h, w_down)
+
+
+def add_fp16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """fp16(a + b) for fp16 operands: the exact sum rounded once, as torch's
+    fp16 ``residual + hidden_states`` (real_fuse.py:82,102) rounds it."""
+    af = np.asarray(a, dtype=np.float16).astype(np.float64)
+    bf = np.asarray(b, dtype=np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):
+        return (af + bf).astype(np.float16)
+
+
+def after_stage(attn: np.ndarray, residual: np.ndarray, w_o: np.ndarray, norm_w: np.ndarray,
+                eps: float, w_gate: np.ndarray, w_up: np.ndarray, w_down: np.ndarray):
+    """(x2, rms, h, out) of the decoder layer after attention
+    (real_fuse.py:77-103): x2 = residual + fp16(attn @ W_o); rms, h and the
+    down product as mlp_forward(x2); out = x2 + fp16(down product)."""
+    x2 = add_fp16(residual, gptq.gemm_ref(attn, w_o).astype(np.float16))
+    rms, h, d = mlp_forward(x2, norm_w, eps, w_gate, w_up, w_down)
+    return x2, rms, h, add_fp16(x2, d.astype(np.float16))

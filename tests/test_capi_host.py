@@ -28,11 +28,11 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 14, names
+    assert len(names) == 15, names
     for name in names:
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, name
-    assert lib.dw4_abi_version() == 2
+    assert lib.dw4_abi_version() == 3
 
 
 def test_strerror_names_every_status():
@@ -112,6 +112,21 @@ def test_stage_entry_points_validate_before_launch():
     assert lib.dw4_mlp_forward(1, fake, 4096, fake, 1e-5, fake, 4096, ctypes.byref(g),
                                ctypes.byref(g), ctypes.byref(down), None, 0,
                                None) == _lib.DW4_ERR_INVALID_ARG
+    # after-attention stage: o->n must equal gate->k and down->n
+    o, d = item(k=4096, n=4096), item(k=11008, n=4096)
+    o_bad = item(k=4096, n=5120)
+    assert lib.dw4_decoder_after_stage(1, fake, 4096, fake, 4096, ctypes.byref(o_bad), fake, 1e-5,
+                                       fake, 4096, ctypes.byref(g), ctypes.byref(g),
+                                       ctypes.byref(d), None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_decoder_after_stage(1, fake, 4096, None, 4096, ctypes.byref(o), fake, 1e-5,
+                                       fake, 4096, ctypes.byref(g), ctypes.byref(g),
+                                       ctypes.byref(d), None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_decoder_after_stage(1, fake, 4096, fake, 4096, ctypes.byref(o), fake, -1.0,
+                                       fake, 4096, ctypes.byref(g), ctypes.byref(g),
+                                       ctypes.byref(d), None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+    assert lib.dw4_decoder_after_stage(0, fake, 4096, fake, 4096, ctypes.byref(o), fake, 1e-5,
+                                       fake, 4096, ctypes.byref(g), ctypes.byref(g),
+                                       ctypes.byref(d), None, 0, None) == _lib.DW4_OK
 
 
 @pytest.mark.parametrize("k,g", [(256, 32), (4096, 128), (13824, 128)])

@@ -532,3 +532,61 @@ def test_stage_composition_on_identity_weights():
     from scipy.special import expit
     assert np.array_equal(h.view(np.uint16), (r * expit(r) * 2 * r).astype(np.float16).view(np.uint16))
     assert np.array_equal(out.astype(np.float16), h)
+
+
+def _after_stage_checks(fn) -> list:
+    """Failures of an after_stage candidate on identity and zero weights, where
+    every intermediate has a closed form."""
+    bad = []
+    k = 64
+    rng = np.random.default_rng(9)
+    attn = rng.standard_normal((2, k)).astype(np.float16)
+    res = rng.standard_normal((2, k)).astype(np.float16)
+    nw = (rng.standard_normal(k) * 0.2 + 1).astype(np.float16)
+    eye, two, zero = _identity_layer(k, 1.0), _identity_layer(k, 2.0), _identity_layer(k, 0.0)
+    from scipy.special import expit
+    x2, rms, h, out = fn(attn, res, eye, nw, 1e-5, eye, two, eye)
+    # o = I: x2 is the fp16 sum of the residual and the attention output
+    if not np.array_equal(x2.view(np.uint16),
+                          (res.astype(np.float64) + attn.astype(np.float64)).astype(np.float16).view(np.uint16)):
+        bad.append("x2 = residual + attn")
+    # the norm is taken of x2, not of the attention output or the residual
+    if not np.array_equal(rms.view(np.uint16), stage.rms_norm(x2, nw, 1e-5).view(np.uint16)):
+        bad.append("rms of x2")
+    r = rms.astype(np.float64)
+    if not np.array_equal(h.view(np.uint16), (r * expit(r) * 2 * r).astype(np.float16).view(np.uint16)):
+        bad.append("h = silu(gate) * up")
+    # down = I: out = x2 + h, rounded once
+    if not np.array_equal(out.view(np.uint16),
+                          (x2.astype(np.float64) + h.astype(np.float64)).astype(np.float16).view(np.uint16)):
+        bad.append("out = x2 + h")
+    # zero o: x2 is the residual itself; zero down: out is x2
+    x2z, _, _, outz = fn(attn, res, zero, nw, 1e-5, eye, two, zero)
+    if not np.array_equal(x2z.view(np.uint16), res.view(np.uint16)):
+        bad.append("zero o")
+    if not np.array_equal(outz.view(np.uint16), x2z.view(np.uint16)):
+        bad.append("zero down")
+    return bad
+
+
+def test_after_stage_pinned():
+    assert _after_stage_checks(stage.after_stage) == []
+    # the fp16 sum is the exactly rounded sum (a library fp16 add agrees)
+    import torch
+    rng = np.random.default_rng(10)
+    a = (rng.standard_normal(4096) * 50).astype(np.float16)
+    b = (rng.standard_normal(4096) * 0.01).astype(np.float16)
+    ref = (torch.from_numpy(a) + torch.from_numpy(b)).numpy()
+    assert np.array_equal(stage.add_fp16(a, b).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("name", ["no_residual", "norm_of_attn", "out_from_residual"])
+def test_after_stage_checks_catch_planted_mistakes(name):
+    def mutant(attn, res, w_o, nw, eps, wg, wu, wd):
+        o = gptq.gemm_ref(attn, w_o).astype(np.float16)
+        x2 = o if name == "no_residual" else stage.add_fp16(res, o)
+        src = stage.add_fp16(attn, np.zeros_like(attn)) if name == "norm_of_attn" else x2
+        rms, h, d = stage.mlp_forward(src, nw, eps, wg, wu, wd)
+        base = res if name == "out_from_residual" else x2
+        return x2, rms, h, stage.add_fp16(base, d.astype(np.float16))
+    assert _after_stage_checks(mutant) != []
