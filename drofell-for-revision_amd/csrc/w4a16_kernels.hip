@@ -145,7 +145,9 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
 
   const int xupc = M * 16;  // 16-byte activation units per chunk
   const int xunits = nch * xupc;
-  const int munits = nch * rec;
+  // group size >= 128: a chunk's scale and zero words travel with its
+  // weights in the ring (no staging); smaller groups stage their records
+  const int munits = G128 ? 0 : nch * rec;
   auto x_unit = [&](int u) -> h8 {
     const int i = u / xupc;
     const int r = u - i * xupc;
@@ -179,12 +181,26 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
     if (lane + 64 * b < munits) mv[b] = m_word(lane + 64 * b);
 
   // weight ring.  With U >= 2 the host guarantees every wave at least U
-  // chunks, so the prologue loads are unconditional.
+  // chunks, so the prologue loads are unconditional.  Each slot holds the
+  // lane's 4 packed words and, for groups of 128 or more, the dword with
+  // its column's scale and the word with its column's stored zero.
   const u4* qp = pq + ((size_t)s * KC + c0) * 64 + lane;
+  const uint32_t* sp = ps32 + (size_t)s * G * 8 + (j >> 1);
+  const uint32_t* zp = pz + (size_t)s * G * 2 + (j >> 3);
   u4 qb[U];
+  uint32_t sb[U], zb[U];
+  auto ring_load = [&](u4& q, uint32_t& sw, uint32_t& zw, int i) {
+    const int c = wave + i * WAVES;
+    q = __builtin_nontemporal_load(qp + (size_t)c * 64);
+    if (G128) {
+      const int g = ((c0 + c) * kChunkK) / gs;
+      sw = sp[(size_t)g * 8];
+      zw = zp[(size_t)g * 2];
+    }
+  };
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (U >= 2 || u < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + u * WAVES) * 64);
+    if (U >= 2 || u < nch) ring_load(qb[u], sb[u], zb[u], u);
 
 #pragma unroll
   for (int b = 0; b < kXBatch; ++b)
@@ -226,17 +242,18 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   for (int mt = 0; mt < MT; ++mt) tot[mt] = f4{0.f, 0.f, 0.f, 0.f};
 
   // One chunk (the wave's i-th): 4 k-steps of 32 rows; w holds this lane's
-  // 4 packed words.
-  auto chunk = [&](const u4 w, int i) {
+  // 4 packed words, sw/zw its scale and zero words (groups >= 128).
+  const int hsh = (j & 1) * 16;
+  auto chunk = [&](const u4 w, uint32_t sw, uint32_t zw, int i) {
     const _Float16* xc = xw + (size_t)i * M * kLdx;
     const uint32_t* mr = mw + i * rec;
     f4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
     if (G128) {
-      const float sc = (float)reinterpret_cast<const _Float16*>(mr)[j];
+      const float sc = (float)as_h((uint16_t)(sw >> hsh));
       h2 nz1024, nz64;
-      zero_consts(mr[8 + (j >> 3)], zsh, nz1024, nz64);
+      zero_consts(zw, zsh, nz1024, nz64);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const h8 b = centered8(w[t], nz1024, nz64, magic);
@@ -283,8 +300,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   for (; i0 + 2 * U <= nch; i0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      chunk(qb[u], i0 + u);  // consume, then refill the same registers
-      qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + (i0 + u + U) * WAVES) * 64);
+      chunk(qb[u], sb[u], zb[u], i0 + u);  // consume, then refill the same registers
+      ring_load(qb[u], sb[u], zb[u], i0 + u + U);
     }
   }
   // Drain: at most 2U - 1 chunks left; refills only where a chunk remains.
@@ -292,14 +309,14 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   for (int u = 0; u < U; ++u) {
     const int i = i0 + u;
     if (i < nch) {
-      chunk(qb[u], i);
-      if (i + U < nch) qb[u] = __builtin_nontemporal_load(qp + (size_t)(wave + (i + U) * WAVES) * 64);
+      chunk(qb[u], sb[u], zb[u], i);
+      if (i + U < nch) ring_load(qb[u], sb[u], zb[u], i + U);
     }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int i = i0 + U + u;
-    if (i < nch) chunk(qb[u], i);
+    if (i < nch) chunk(qb[u], sb[u], zb[u], i);
   }
 
   __syncthreads();  // staged activations are dead; reuse LDS for the reduction
