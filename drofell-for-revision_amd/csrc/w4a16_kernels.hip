@@ -362,20 +362,25 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
 // per 32-row k-step, from L2) into the same register ring as the weights,
 // and SS adjacent strips share them, so no LDS is needed until the final
 // cross-wave reduction and K is never split.
-// PAIR (SS = 2): workgroup s holds strip s of item 0 (gate) and of item 1
+// Pair mode (SS = 2): workgroup s holds strip s of item 0 (gate) and of item 1
 // (up), which share perm, and writes fp16(silu(gate) * up) to item 0's
 // output; the two products never reach memory.
 // ---------------------------------------------------------------------------
 
-template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, bool PAIR>
+// MODE: kRegSingle (one matrix, item 0 read directly), kRegGroup (several
+// matrices, item looked up per workgroup) or kRegPair (gate/up, above).
+constexpr int kRegSingle = 0, kRegGroup = 1, kRegPair = 2;
+
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d, int K,
                   int gs, int G) {
+  constexpr bool PAIR = MODE == kRegPair;
   static_assert(!PAIR || SS == 2, "a pair workgroup holds one strip of each matrix");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
   constexpr int SPG = 4 / GPC;  // 32-row k-steps per group
-  const int item = PAIR ? 0 : item_of(d, blockIdx.x);
+  const int item = MODE == kRegGroup ? item_of(d, blockIdx.x) : 0;
   const int s0 = PAIR ? (int)blockIdx.x : ((int)blockIdx.x - pick(d.wg0, item)) * SS;
   const int NS = pick(d.n, item) / kStripN;
   const int32_t* __restrict__ perm = pick(d.perm, item);
@@ -557,12 +562,12 @@ static Items make_items(const GroupArgs& g, int ss) {
   return d;
 }
 
-template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, bool PAIR>
+template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
 static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, hipStream_t stream) {
   const GemmArgs& a = g.a[0];
-  const dim3 grid((unsigned)(PAIR ? a.N / kStripN : d.wg0[d.count]));
+  const dim3 grid((unsigned)(MODE == kRegPair ? a.N / kStripN : d.wg0[d.count]));
   const size_t smem = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
-  decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT, PAIR><<<grid, WAVES * 64, smem, stream>>>(
+  decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT, MODE><<<grid, WAVES * 64, smem, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, d, a.K, a.gs, a.G);
   return hipGetLastError();
 }
@@ -579,61 +584,74 @@ constexpr int decode_reg_umax(int mt, int waves, int gpc, bool act) {
 }
 
 // Ring depth U: the deepest allowed, at most the chunks of the shortest wave.
-template <int MT, int WAVES, int SS, int GPC, bool ACT, bool PAIR>
+template <int MT, int WAVES, int SS, int GPC, bool ACT, int MODE>
 static hipError_t launch_decode_reg_u(const GroupArgs& g, const Items& d, hipStream_t stream) {
   const int per_wave = (g.a[0].K / kChunkK) / WAVES;
   constexpr int umax = decode_reg_umax(MT, WAVES, GPC, ACT);
   if constexpr (umax >= 4) {
-    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT, PAIR>(g, d, stream);
+    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT, MODE>(g, d, stream);
   }
   if constexpr (umax >= 2) {
-    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT, PAIR>(g, d, stream);
+    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT, MODE>(g, d, stream);
   }
   // 16 waves are planned only where every wave gets two chunks or more
   if constexpr (WAVES == 16) return hipErrorInvalidValue;
-  else return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT, PAIR>(g, d, stream);
+  else return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT, MODE>(g, d, stream);
 }
 
-template <int MT, int WAVES, int SS, bool ACT, bool PAIR>
+template <int MT, int WAVES, int SS, bool ACT, int MODE>
 static hipError_t launch_decode_reg_g(const GroupArgs& g, const Items& d, hipStream_t stream) {
   const int gs = g.a[0].gs;
   const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
-  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, PAIR>(g, d, stream);
-  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, PAIR>(g, d, stream);
-  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT, PAIR>(g, d, stream);
+  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, MODE>(g, d, stream);
+  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, MODE>(g, d, stream);
+  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT, MODE>(g, d, stream);
 }
 
-template <int MT, int WAVES, int SS, bool PAIR = false>
+template <int MT, int WAVES, int SS, int MODE>
 static hipError_t launch_decode_reg_w(const GroupArgs& g, hipStream_t stream) {
   if (g.a[0].perm == nullptr) {
-    const Items d = make_items(g, PAIR ? 1 : SS);
-    return launch_decode_reg_g<MT, WAVES, SS, false, PAIR>(g, d, stream);
+    const Items d = make_items(g, MODE == kRegPair ? 1 : SS);
+    return launch_decode_reg_g<MT, WAVES, SS, false, MODE>(g, d, stream);
   }
   // act-order gathers for four tiles and two strips do not fit the registers
-  if constexpr (MT == 4 && SS == 2 && !PAIR) {
+  if constexpr (MT == 4 && SS == 2 && MODE != kRegPair) {
     const Items d = make_items(g, 1);
-    return launch_decode_reg_g<MT, WAVES, 1, true, false>(g, d, stream);
+    return launch_decode_reg_g<MT, WAVES, 1, true, MODE>(g, d, stream);
   } else {
-    const Items d = make_items(g, PAIR ? 1 : SS);
-    return launch_decode_reg_g<MT, WAVES, SS, true, PAIR>(g, d, stream);
+    const Items d = make_items(g, MODE == kRegPair ? 1 : SS);
+    return launch_decode_reg_g<MT, WAVES, SS, true, MODE>(g, d, stream);
   }
 }
 
-template <int MT>
+template <int MT, int MODE>
 static hipError_t launch_decode_reg_mt(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
-  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2>(g, stream) : launch_decode_reg_w<MT, 8, 1>(g, stream);
+  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2, MODE>(g, stream)
+                   : launch_decode_reg_w<MT, 8, 1, MODE>(g, stream);
+}
+
+// Grouped launches come from the automatic path, which takes decode only up
+// to M = 32 (two row tiles).
+template <int MT>
+static hipError_t launch_decode_reg_m(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
+  if (g.count == 1) return launch_decode_reg_mt<MT, kRegSingle>(g, p, stream);
+  if constexpr (MT <= 2) return launch_decode_reg_mt<MT, kRegGroup>(g, p, stream);
+  else return hipErrorInvalidValue;
 }
 
 hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
   const int M = g.a[0].M;
   if (M <= 16) {
-    if (p.waves == 16) return launch_decode_reg_w<1, 16, 1>(g, stream);  // planner: ss == 1
-    return launch_decode_reg_mt<1>(g, p, stream);
+    if (p.waves == 16) {  // planner: ss == 1
+      return g.count == 1 ? launch_decode_reg_w<1, 16, 1, kRegSingle>(g, stream)
+                          : launch_decode_reg_w<1, 16, 1, kRegGroup>(g, stream);
+    }
+    return launch_decode_reg_m<1>(g, p, stream);
   }
   if (p.waves != 8) return hipErrorInvalidValue;
-  if (M <= 32) return launch_decode_reg_mt<2>(g, p, stream);
-  if (M <= 48) return launch_decode_reg_mt<3>(g, p, stream);
-  if (M <= 64) return launch_decode_reg_mt<4>(g, p, stream);
+  if (M <= 32) return launch_decode_reg_m<2>(g, p, stream);
+  if (M <= 48) return launch_decode_reg_m<3>(g, p, stream);
+  if (M <= 64) return launch_decode_reg_m<4>(g, p, stream);
   return hipErrorInvalidValue;
 }
 
@@ -643,8 +661,8 @@ hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipS
   gp.a[0].y = h;  // the pair's output goes where item 0's would
   gp.a[0].ldy = ldh;
   const int M = g.a[0].M;
-  if (M <= 16) return launch_decode_reg_w<1, 8, 2, true>(gp, stream);
-  if (M <= kPairMaxM) return launch_decode_reg_w<2, 8, 2, true>(gp, stream);
+  if (M <= 16) return launch_decode_reg_w<1, 8, 2, kRegPair>(gp, stream);
+  if (M <= kPairMaxM) return launch_decode_reg_w<2, 8, 2, kRegPair>(gp, stream);
   return hipErrorInvalidValue;
 }
 
