@@ -198,10 +198,18 @@ int dw4_repack(int k, int n, int group_size, const int32_t* qweight, const int32
   return status_of(e);
 }
 
-int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, const uint16_t* x,
-                  int64_t ldx, const int32_t* packed_qweight, const int32_t* packed_zeros,
-                  const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias,
-                  uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// dw4_gemm_path with an optional residual added after the rounding of the
+// product (y = fp16(fp16(x @ W (+ bias)) + res)); res is y itself (same
+// stride) or does not overlap it.
+int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const uint16_t* x,
+             int64_t ldx, const int32_t* packed_qweight, const int32_t* packed_zeros,
+             const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias,
+             uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldres, void* workspace,
+             size_t workspace_bytes, void* stream) {
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;
   if (path < DW4_PATH_AUTO || path > DW4_PATH_PREFILL || m < 0 || split_k < 0)
@@ -229,6 +237,8 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
   a.bias = bias;
   a.y = y;
   a.ldy = ldy;
+  a.res = res;
+  a.ldres = ldres;
 
   if (decode) {
     const dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
@@ -245,6 +255,19 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, co
   dw4::PrefillPlan plan = plan_prefill(m, k, n, split_k, workspace ? workspace_bytes : 0, true);
   if (plan.splits > 1 && !aligned16(workspace)) plan.splits = 1;
   return status_of(dw4::launch_prefill(a, plan, workspace, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size, const uint16_t* x,
+                  int64_t ldx, const int32_t* packed_qweight, const int32_t* packed_zeros,
+                  const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  return gemm_run(path, split_k, m, k, n, group_size, x, ldx, packed_qweight, packed_zeros,
+                  packed_scales, perm, bias, y, ldy, nullptr, 0, workspace, workspace_bytes,
+                  stream);
 }
 
 int dw4_gemm(int m, int k, int n, int group_size, const uint16_t* x, int64_t ldx,
@@ -317,10 +340,18 @@ dw4::GemmArgs args_of(int m, const uint16_t* x, int64_t ldx, const dw4_item* it)
 }
 
 int gemm_item(int m, const uint16_t* x, int64_t ldx, const dw4_item* it, void* ws, size_t wsb,
-              void* stream) {
-  return dw4_gemm_path(DW4_PATH_AUTO, 0, m, it->k, it->n, it->group_size, x, ldx,
-                       it->packed_qweight, it->packed_zeros, it->packed_scales, it->perm, it->bias,
-                       it->y, it->ldy, ws, wsb, stream);
+              void* stream, const uint16_t* res = nullptr, int64_t ldres = 0) {
+  return gemm_run(DW4_PATH_AUTO, 0, m, it->k, it->n, it->group_size, x, ldx, it->packed_qweight,
+                  it->packed_zeros, it->packed_scales, it->perm, it->bias, it->y, it->ldy, res,
+                  ldres, ws, wsb, stream);
+}
+
+// Whether the fp16 [m, n] views a (row stride lda) and b (ldb) share bytes.
+bool overlap(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int m, int n) {
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  const uintptr_t a1 = a0 + ((size_t)(m - 1) * lda + n) * sizeof(uint16_t);
+  const uintptr_t b1 = b0 + ((size_t)(m - 1) * ldb + n) * sizeof(uint16_t);
+  return a0 < b1 && b0 < a1;
 }
 
 
@@ -424,9 +455,16 @@ int dw4_attention_qkv_stage(int m, const uint16_t* x, int64_t ldx, const uint16_
   return dw4_gemm_group(3, items, m, rms, ldr, workspace, workspace_bytes, stream);
 }
 
-int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
-                    uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
-                    const dw4_item* down, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// dw4_mlp_forward; res (if not NULL, not overlapping down->y) is added to
+// the down product in its epilogue.
+int mlp_run(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
+            uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+            const dw4_item* down, const uint16_t* res, int64_t ldres, void* workspace,
+            size_t workspace_bytes, void* stream) {
   if (gate == nullptr || up == nullptr || down == nullptr) return DW4_ERR_INVALID_ARG;
   int st = check_item(down);
   if (st == DW4_OK) st = check_output(down);
@@ -438,7 +476,18 @@ int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_
     st = dw4_gemm_silu_mul(m, rms, ldr, gate, up, gate->y, gate->ldy, workspace, workspace_bytes,
                            stream);
   if (st != DW4_OK) return st;
-  return gemm_item(m, gate->y, gate->ldy, down, workspace, workspace_bytes, stream);
+  return gemm_item(m, gate->y, gate->ldy, down, workspace, workspace_bytes, stream, res, ldres);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_w, float eps,
+                    uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
+                    const dw4_item* down, void* workspace, size_t workspace_bytes, void* stream) {
+  return mlp_run(m, x, ldx, norm_w, eps, rms, ldr, gate, up, down, nullptr, 0, workspace,
+                 workspace_bytes, stream);
 }
 
 int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint16_t* residual,
@@ -459,19 +508,20 @@ int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint
     return DW4_ERR_INVALID_ARG;
   if (!(eps >= 0.0f) || norm_w == nullptr || rms == nullptr) return DW4_ERR_INVALID_ARG;
   if (m == 0) return DW4_OK;
+  // x2 (o->y) is read while down's product is written
+  if (overlap(o->y, o->ldy, down->y, down->ldy, m, o->n)) return DW4_ERR_INVALID_ARG;
   st = check_x(attn, lda, o->k);
   if (st != DW4_OK) return st;
-  // o_proj, + residual, mlp_forward, + residual (real_fuse.py:80-103)
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  st = gemm_item(m, attn, lda, o, workspace, workspace_bytes, stream);
-  if (st == DW4_OK)
-    st = status_of(dw4::launch_add(residual, ldres, o->y, o->ldy, o->y, o->ldy, m, o->n, s));
-  if (st == DW4_OK)
-    st = dw4_mlp_forward(m, o->y, o->ldy, norm_w, eps, rms, ldr, gate, up, down, workspace,
-                         workspace_bytes, stream);
+  // o_proj + residual, mlp_forward + residual (real_fuse.py:80-103), the
+  // residual adds in the GEMM epilogues.  Each output element is read from
+  // the residual and written by the same thread, so o->y may be the
+  // residual itself; a partial overlap is rejected.
+  const bool same = residual == o->y && ldres == o->ldy;
+  if (!same && overlap(residual, ldres, o->y, o->ldy, m, o->n)) return DW4_ERR_INVALID_ARG;
+  st = gemm_item(m, attn, lda, o, workspace, workspace_bytes, stream, residual, ldres);
   if (st != DW4_OK) return st;
-  return status_of(dw4::launch_add(o->y, o->ldy, down->y, down->ldy, down->y, down->ldy, m,
-                                   down->n, s));
+  return mlp_run(m, o->y, o->ldy, norm_w, eps, rms, ldr, gate, up, down, o->y, o->ldy, workspace,
+                 workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -89,6 +89,15 @@ __device__ __forceinline__ int item_of(const Items& d, int b) {
          (d.count > 3 && b >= d.wg0[3]);
 }
 
+// Eight fp16 sums a + b of packed halves, each rounded once (v_pk_add_f16),
+// as an fp16 tensor add rounds them.
+__device__ __forceinline__ u4 add_h8(u4 a, u4 b) {
+  u4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = __builtin_bit_cast(uint32_t, as_h2(a[e]) + as_h2(b[e]));
+  return r;
+}
+
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
 
 }  // namespace dw4

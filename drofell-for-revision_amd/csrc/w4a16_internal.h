@@ -40,6 +40,11 @@ struct GemmArgs {
   const uint16_t* bias;
   uint16_t* y;
   int64_t ldy;
+  // optional residual r [M, N] (row stride ldres): y = fp16(fp16(x @ W (+ bias)) + r).
+  // r is y itself (same stride; every element is read and then written by
+  // one thread) or does not overlap y.
+  const uint16_t* res = nullptr;
+  int64_t ldres = 0;
 };
 
 // Matrices launched together.  They share x, M, K and the group size; each
@@ -60,6 +65,8 @@ struct Items {
   const uint16_t* bias[kGroupMax];
   uint16_t* y[kGroupMax];
   int64_t ldy[kGroupMax];
+  const uint16_t* res[kGroupMax];
+  int64_t ldres[kGroupMax];
   int n[kGroupMax];
   int wg0[kGroupMax + 1];
   int count;
@@ -169,10 +176,6 @@ constexpr size_t kWsHeadBytes = kSplitCounters * sizeof(int);
 inline size_t split_ws_bytes(int splits, size_t plane_floats) {
   return splits > 1 ? kWsHeadBytes + (size_t)splits * plane_floats * sizeof(float) : 0;
 }
-
-// y = fp16(a + b) over [m, n] (row strides lda, ldb, ldy); y may alias a or b.
-hipError_t launch_add(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* y,
-                      int64_t ldy, int m, int n, hipStream_t stream);
 
 hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* ws,
                           hipStream_t stream);

@@ -127,6 +127,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   const uint16_t* __restrict__ bias = GRP ? pick(d.bias, item) : d.bias[0];
   uint16_t* __restrict__ y = GRP ? pick(d.y, item) : d.y[0];
   const int64_t ldy = GRP ? pick(d.ldy, item) : d.ldy[0];
+  const uint16_t* __restrict__ res = GRP ? pick(d.res, item) : d.res[0];
+  const int64_t ldres = GRP ? pick(d.ldres, item) : d.ldres[0];
   const int split = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -346,6 +348,7 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
     if (direct) {
       _Float16 out = (_Float16)sum;
       if (bias != nullptr) out = out + as_h(bias[n]);
+      if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
       y[(size_t)m * ldy + n] = h_bits(out);
     } else {
       part[((size_t)split * M + m) * N + n] = sum;
@@ -522,6 +525,8 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
     const uint16_t* __restrict__ bias = pick(d.bias, item);
     uint16_t* __restrict__ y = pick(d.y, item);
     const int64_t ldy = pick(d.ldy, item);
+    const uint16_t* __restrict__ res = pick(d.res, item);
+    const int64_t ldres = pick(d.ldres, item);
     for (int idx = tid; idx < SS * MT * 256; idx += T) {
       const int sm = idx >> 8;  // ss * MT + mt
       const int ss = sm / MT;
@@ -536,6 +541,7 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
       const int n = st * kStripN + llo;
       _Float16 out = (_Float16)wave_sum(sm, L, r);
       if (bias != nullptr) out = out + as_h(bias[n]);
+      if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
       y[(size_t)m * ldy + n] = h_bits(out);
     }
   }
@@ -555,6 +561,8 @@ static Items make_items(const GroupArgs& g, int ss) {
     d.bias[i] = a.bias;
     d.y[i] = a.y;
     d.ldy[i] = a.ldy;
+    d.res[i] = a.res;
+    d.ldres[i] = a.ldres;
     d.n[i] = a.N;
     const int wgs = i < g.count ? (a.N / kStripN + ss - 1) / ss : 0;
     d.wg0[i + 1] = d.wg0[i] + wgs;
@@ -689,7 +697,8 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                const int32_t* __restrict__ perm,
                const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
                const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
-               uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
+               uint16_t* __restrict__ y, int64_t ldy,
+               const uint16_t* __restrict__ res, int64_t ldres, float* __restrict__ part,
                int* __restrict__ counters, int K, int N, int gs, int G, int chunks_per_split,
                int mtiles, int ntiles) {
   constexpr int BM = 16 * MT2;
@@ -878,7 +887,9 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   constexpr int SEG = TW / 8;      // 16-byte segments per tile row
   constexpr int RPP = 64 / SEG;    // tile rows per 64-lane pass
   static_assert(4 * 16 * MT2 * TW <= 2 * BM * kLda, "output tiles fit in the activation buffers");
-  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0);
+  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0) &&
+                     (res == nullptr ||
+                      (((reinterpret_cast<uintptr_t>(res) & 15) == 0) && (ldres % 8 == 0)));
   auto write_tile = [&](auto&& val) {  // val(mt, si, r): fp32 result of that accumulator slot
     _Float16* T = &As[0][0] + wave * (16 * MT2 * TW);
 #pragma unroll
@@ -899,15 +910,23 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       const int m = m0 + row;
       const int strip = strip0 + seg / 2;
       if (m < M && strip < NS) {
-        const u4 v = *(const u4*)&T[row * TW + seg * 8];
-        uint16_t* dst = y + (size_t)m * ldy + strip * kStripN + (seg & 1) * 8;
+        u4 v = *(const u4*)&T[row * TW + seg * 8];
+        const int col = strip * kStripN + (seg & 1) * 8;
+        uint16_t* dst = y + (size_t)m * ldy + col;
+        const uint16_t* rsrc = res != nullptr ? res + (size_t)m * ldres + col : nullptr;
         if (vec_y) {
+          if (rsrc != nullptr) v = add_h8(v, *(const u4*)rsrc);
           *(u4*)dst = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            dst[2 * e] = (uint16_t)(v[e] & 0xFFFFu);
-            dst[2 * e + 1] = (uint16_t)(v[e] >> 16);
+            _Float16 lo = as_h((uint16_t)(v[e] & 0xFFFFu)), hi = as_h((uint16_t)(v[e] >> 16));
+            if (rsrc != nullptr) {
+              lo = lo + as_h(rsrc[2 * e]);
+              hi = hi + as_h(rsrc[2 * e + 1]);
+            }
+            dst[2 * e] = h_bits(lo);
+            dst[2 * e + 1] = h_bits(hi);
           }
         }
       }
@@ -1021,7 +1040,8 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                  const int32_t* __restrict__ perm,
                  const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
                  const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
-                 uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
+                 uint16_t* __restrict__ y, int64_t ldy,
+                 const uint16_t* __restrict__ res, int64_t ldres, float* __restrict__ part,
                  int* __restrict__ counters, int K, int N, int gs, int G, int chunks_per_split,
                  int mtiles, int ntiles) {
   constexpr int S = 2 * P;               // 16-column strips per wave
@@ -1208,7 +1228,9 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     const int st = strip0 + 2 * p + hi;
     bv[p] = (bias != nullptr && st < NS) ? as_h(bias[st * kStripN + j]) : (_Float16)0.f;
   }
-  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0);
+  const bool vec_y = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0) &&
+                     (res == nullptr ||
+                      (((reinterpret_cast<uintptr_t>(res) & 15) == 0) && (ldres % 8 == 0)));
   auto write_tile = [&](auto&& val) {  // val(mt, p, i): fp32 result of that accumulator slot
     _Float16* T = &As[0][0] + wave * (BM * TW);
 #pragma unroll
@@ -1229,15 +1251,23 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       const int m = m0 + row;
       const int strip = strip0 + seg / 2;
       if (m < M && strip < NS) {
-        const u4 v = *(const u4*)&T[row * TW + seg * 8];
-        uint16_t* dst = y + (size_t)m * ldy + strip * kStripN + (seg & 1) * 8;
+        u4 v = *(const u4*)&T[row * TW + seg * 8];
+        const int col = strip * kStripN + (seg & 1) * 8;
+        uint16_t* dst = y + (size_t)m * ldy + col;
+        const uint16_t* rsrc = res != nullptr ? res + (size_t)m * ldres + col : nullptr;
         if (vec_y) {
+          if (rsrc != nullptr) v = add_h8(v, *(const u4*)rsrc);
           *(u4*)dst = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            dst[2 * e] = (uint16_t)(v[e] & 0xFFFFu);
-            dst[2 * e + 1] = (uint16_t)(v[e] >> 16);
+            _Float16 lo = as_h((uint16_t)(v[e] & 0xFFFFu)), hi = as_h((uint16_t)(v[e] >> 16));
+            if (rsrc != nullptr) {
+              lo = lo + as_h(rsrc[2 * e]);
+              hi = hi + as_h(rsrc[2 * e + 1]);
+            }
+            dst[2 * e] = h_bits(lo);
+            dst[2 * e + 1] = h_bits(hi);
           }
         }
       }
@@ -1306,7 +1336,8 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 
 __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
                               const uint16_t* __restrict__ bias,
-                              uint16_t* __restrict__ y, int64_t ldy) {
+                              uint16_t* __restrict__ y, int64_t ldy,
+                              const uint16_t* __restrict__ res, int64_t ldres) {
   const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t total = (size_t)M * N;
   if (o >= total) return;
@@ -1316,6 +1347,7 @@ __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M,
   const int n = (int)(o % N);
   _Float16 out = (_Float16)sum;
   if (bias != nullptr) out = out + as_h(bias[n]);
+  if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
   y[(size_t)m * ldy + n] = h_bits(out);
 }
 
@@ -1410,7 +1442,8 @@ static hipError_t launch_decode_cfg(const GroupArgs& g, const DecodePlan& p, flo
   if (err != hipSuccess || p.splits == 1) return err;
   const size_t total = (size_t)a.M * a.N;
   reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(part, p.splits, a.M, a.N,
-                                                                     a.bias, a.y, a.ldy);
+                                                                     a.bias, a.y, a.ldy,
+                                                                     a.res, a.ldres);
   return hipGetLastError();
 }
 
@@ -1497,7 +1530,7 @@ static hipError_t launch_prefill_cfg(const GemmArgs& a, int splits, void* ws, hi
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
   prefill_kernel<MT2, S, PB, GPC, ACT><<<grid, 256, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
-      a.bias, a.y, a.ldy, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
+      a.bias, a.y, a.ldy, a.res, a.ldres, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   return hipGetLastError();
 }
 
@@ -1518,7 +1551,7 @@ static hipError_t launch_prefill32_cfg(const GemmArgs& a, int splits, void* ws, 
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
   prefill32_kernel<MT3, P, PB, GPC, ACT><<<grid, 256, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, a.perm, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps,
-      a.bias, a.y, a.ldy, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
+      a.bias, a.y, a.ldy, a.res, a.ldres, part, counters, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   return hipGetLastError();
 }
 
@@ -1641,24 +1674,6 @@ rms_norm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __r
 hipError_t launch_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,
                            uint16_t* y, int64_t ldy, int m, int k, hipStream_t stream) {
   rms_norm_kernel<<<(unsigned)m, 256, 0, stream>>>(x, ldx, w, eps, y, ldy, k);
-  return hipGetLastError();
-}
-
-// y = fp16(a + b), one element per thread (the fp16 residual adds of the
-// reference's decoder, real_fuse.py:82,102).
-__global__ void add_kernel(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                           uint16_t* y, int64_t ldy, int m, int n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)m * n) return;
-  const int64_t r = i / n;
-  const int64_t c = i - r * n;
-  y[r * ldy + c] = h_bits(as_h(a[r * lda + c]) + as_h(b[r * ldb + c]));
-}
-
-hipError_t launch_add(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* y,
-                      int64_t ldy, int m, int n, hipStream_t stream) {
-  const int64_t total = (int64_t)m * n;
-  add_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(a, lda, b, ldb, y, ldy, m, n);
   return hipGetLastError();
 }
 

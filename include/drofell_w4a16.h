@@ -225,7 +225,11 @@ int dw4_mlp_forward(int m, const uint16_t* x, int64_t ldx, const uint16_t* norm_
  * attn fp16 [m, o->k] (row stride lda), residual fp16 [m, o->n] (ldres).
  * o->n == gate->k == down->n, down->k == gate->n.  up->y receives the up
  * product where gate and up cannot run as one launch (as dw4_gemm_silu_mul).
- * Runs as o_proj, an fp16 add, dw4_mlp_forward and an fp16 add. */
+ * residual may be o->y itself (same stride) or down->y; down->y must not
+ * overlap o->y, nor residual overlap o->y partially (DW4_ERR_INVALID_ARG).
+ * Runs as o_proj and dw4_mlp_forward, each residual add done in the
+ * epilogue of the GEMM before it (rounded after the product, as two fp16
+ * tensor ops round). */
 int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint16_t* residual,
                             int64_t ldres, const dw4_item* o, const uint16_t* norm_w, float eps,
                             uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,

@@ -127,6 +127,10 @@ def test_stage_entry_points_validate_before_launch():
     assert lib.dw4_decoder_after_stage(0, fake, 4096, fake, 4096, ctypes.byref(o), fake, 1e-5,
                                        fake, 4096, ctypes.byref(g), ctypes.byref(g),
                                        ctypes.byref(d), None, 0, None) == _lib.DW4_OK
+    # down->y over o->y (x2 is read while down's product is written)
+    assert lib.dw4_decoder_after_stage(1, fake, 4096, fake, 4096, ctypes.byref(o), fake, 1e-5,
+                                       fake, 4096, ctypes.byref(g), ctypes.byref(g),
+                                       ctypes.byref(d), None, 0, None) == _lib.DW4_ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("k,g", [(256, 32), (4096, 128), (13824, 128)])

@@ -1,7 +1,8 @@
 """GPU parity of the after-attention decoder stage (o_proj + residual,
 rms_norm, gate/up + silu * mul, down + residual; dw4_decoder_after_stage)
-against the oracle, on Llama-2-7B shapes and act-order 13B shapes, M = 1..8,
-and under HIP-graph replay.
+against the oracle, on Llama-2-7B shapes (M = 1..100: decode and prefill
+kernels, with the residual adds in the GEMM epilogues), act-order 13B shapes,
+residual buffers shared with an output, and under HIP-graph replay.
 
 Bars: GEMM-derived outputs within max|y - y_ref| <= 2e-2 * ||y_ref row||_inf;
 the gated product h within 5e-3 * ||h_ref row||_inf; rms within 1e-2 of
@@ -114,14 +115,44 @@ def test_after_stage(hip_device, shape, act):
         assert q4s[1].perm.data_ptr() == q4s[2].perm.data_ptr()  # gate/up share: chained
     ws = [lw[1] for lw in lws]
     wn = norm_weight(hidden, 7)
-    b = _Bufs(8, hidden, inter, hip_device)
-    for m in (1, 2, 3, 4, 8):
+    ms = (1, 2, 3, 4, 8) if act else (1, 2, 3, 4, 8, 16, 33, 64, 100)
+    b = _Bufs(max(ms), hidden, inter, hip_device)
+    for m in ms:
         say(f"after_stage {hidden}x{inter} act={act} M={m}")
         attn = make_x(m, hidden, seed=1100 + m)
         res = (make_x(m, hidden, seed=1200 + m) * 4).to(torch.float16)
         _after(q4s, wn.to(hip_device), attn.to(hip_device), res.to(hip_device), b, m)
         torch.cuda.synchronize()
         _check_after(b, m, attn, res, ws, wn, f"after M={m}")
+
+
+@pytest.mark.parametrize("alias", ["out_is_residual", "x2_is_residual"])
+def test_after_stage_in_place(hip_device, alias):
+    """Buffers a caller may share: the output or the hidden state written
+    over the residual (the o_proj epilogue then reads and writes each
+    element in one thread)."""
+    lws = _layers(4096, 11008, False, 3000)
+    q4s, cache = build([lw[0] for lw in lws], hip_device)
+    ws = [lw[1] for lw in lws]
+    wn = norm_weight(4096, 30)
+    dev = hip_device
+    for m in (1, 40):
+        say(f"after_stage in place {alias} M={m}")
+        attn = make_x(m, 4096, seed=3100 + m)
+        res = (make_x(m, 4096, seed=3200 + m) * 4).to(torch.float16)
+        x2_ref, rms_ref, h_ref, out_ref = stage.after_stage(
+            attn.numpy(), res.numpy(), ws[0], wn.numpy(), EPS, ws[1], ws[2], ws[3])
+        b = _Bufs(m, 4096, 11008, dev)
+        res_d = res.to(dev)
+        if alias == "out_is_residual":
+            b.out = res_d
+        else:
+            b.x2 = res_d
+        _after(q4s, wn.to(dev), attn.to(dev), res_d, b, m)
+        torch.cuda.synchronize()
+        check(b.x2[:m], x2_ref.astype(np.float64), f"in-place M={m} x2")
+        check(b.out[:m], out_ref.astype(np.float64), f"in-place M={m} out")
+        check(b.h[:m], h_ref.astype(np.float64), f"in-place M={m} h", TOL_H)
 
 
 def test_after_stage_graph_replay(hip_device):
