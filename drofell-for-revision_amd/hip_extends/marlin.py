@@ -185,12 +185,34 @@ class MarlinQ4Matrix:
     def set_tuning_params(self, tuning_params: MarlinTuningParams) -> None:
         self.tuning_params = tuning_params
 
+    _MOVED = ("qweight", "qzeros", "scales", "g_idx", "g_idx_sort_indices", "workspace",
+              "dequant_weight_permutation", "dequant_scale_column_map")
+
+    def rebind(self, **tensors: torch.Tensor) -> None:
+        """Point the matrix at moved copies of its tensors (module swap-out
+        and swap-in); nothing is repacked.  Products raise while the tensors
+        are in host memory."""
+        for name in self._MOVED:
+            new, old = tensors[name], getattr(self, name)
+            if new.shape != old.shape or new.dtype != old.dtype:
+                raise ValueError(f"{name}: moved tensor does not match the packed one")
+        devices = {tensors[name].device for name in self._MOVED}
+        if len(devices) != 1:
+            raise ValueError(f"Marlin tensors on several devices: {devices}")
+        for name in self._MOVED:
+            setattr(self, name, tensors[name])
+
+    def _check_resident(self) -> None:
+        if self.qweight.device.type != "cuda":
+            raise RuntimeError("MarlinQ4Matrix is swapped out (its tensors are in host memory)")
+
     def use_reconstructed_forward(self, flattened_tokens: int, *, cache_weight: bool) -> bool:
         return self.tuning_params.use_reconstructed_forward(flattened_tokens,
                                                             cache_weight=cache_weight)
 
     def reconstruct_weight(self, output: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Bit-exact fp16 weight [K, N] in checkpoint row order."""
+        self._check_resident()
         if output is None:
             output = torch.empty((self.in_features, self.out_features), dtype=torch.float16,
                                  device=self.qweight.device)
@@ -205,6 +227,7 @@ class MarlinQ4Matrix:
 
     def direct_matmul(self, x: torch.Tensor) -> torch.Tensor:
         """The packed W4A16 kernel: fp16 [..., K] -> fp16 [..., N]."""
+        self._check_resident()
         x_2d = _aligned_rows(x.reshape(-1, self.in_features).to(torch.float16))
         m = x_2d.shape[0]
         output = torch.empty((m, self.out_features), dtype=torch.float16, device=x.device)

@@ -122,8 +122,12 @@ _perm_lock = threading.Lock()
 _perm_intern: Dict[Tuple[str, int, str], Tuple[torch.Tensor, "weakref.ref[torch.Tensor]"]] = {}
 
 
+def perm_digest(perm_host: torch.Tensor) -> str:
+    return hashlib.sha1(perm_host.numpy().tobytes()).hexdigest()
+
+
 def _shared_perm(perm_host: torch.Tensor, device: torch.device) -> torch.Tensor:
-    key = (str(device), perm_host.numel(), hashlib.sha1(perm_host.numpy().tobytes()).hexdigest())
+    key = (str(device), perm_host.numel(), perm_digest(perm_host))
     with _perm_lock:
         hit = _perm_intern.get(key)
         if hit is not None:
@@ -133,6 +137,38 @@ def _shared_perm(perm_host: torch.Tensor, device: torch.device) -> torch.Tensor:
         dev = perm_host.to(device)
         _perm_intern[key] = (perm_host.clone(), weakref.ref(dev))
         return dev
+
+
+class PermGroup(object):
+    """Matrices whose act-order permutations are equal.
+
+    Module moves (``nn.Module.to`` / ``cuda`` / ``cpu``) copy each module's
+    buffers separately, so after a swap-in every matrix would hold its own
+    copy of the permutation and the fused launches, which pair matrices by
+    the permutation pointer, would no longer pair them.  A moved matrix
+    offers its new tensor to its group and takes the group's tensor when that
+    one already lives on the same device (the contents are equal by
+    construction).
+    """
+
+    def __init__(self) -> None:
+        self.tensor: Optional[torch.Tensor] = None
+
+    def share(self, t: torch.Tensor) -> torch.Tensor:
+        cur = self.tensor
+        if cur is not None and cur.device == t.device and cur.shape == t.shape:
+            return cur
+        self.tensor = t
+        return t
+
+
+_groups_lock = threading.Lock()
+_perm_groups: Dict[Tuple[int, str], PermGroup] = {}
+
+
+def perm_group(numel: int, digest: str) -> PermGroup:
+    with _groups_lock:
+        return _perm_groups.setdefault((numel, digest), PermGroup())
 
 
 class Q4MatrixV2(object):
@@ -182,6 +218,10 @@ class Q4MatrixV2(object):
             # g_idx == k // group_size sorts to the identity: no gather needed
             if not torch.equal(perm_host, torch.arange(height, dtype=torch.int32)):
                 perm = _shared_perm(perm_host, self.device)
+                self.perm_group: Optional[PermGroup] = perm_group(height, perm_digest(perm_host))
+                self.perm_group.share(perm)
+        if perm is None:
+            self.perm_group = None
         self.use_act = perm is not None
         self.perm: torch.Tensor = perm if perm is not None else \
             torch.empty(0, dtype=torch.int32, device=self.device)
@@ -206,6 +246,39 @@ class Q4MatrixV2(object):
         """The handle the fused stage calls take (the reference's ``make_q4``
         pointer, ``exllama.py:203``): the matrix object itself."""
         return self
+
+    def rebind(self, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+               perm: torch.Tensor) -> None:
+        """Point the matrix at moved copies of its packed tensors (a module
+        swapped out to host memory and back in, or moved between devices).
+        The packed layout travels with the tensors, so nothing is repacked;
+        a matrix whose tensors are in host memory refuses products until it
+        is moved back.  A reconstructed fp16 weight is rebuilt on the new
+        device (it is derived data, not swapped)."""
+        if qweight is self.qweight and qzeros is self.qzeros and scales is self.scales \
+                and perm is self.perm:
+            return  # e.g. a dtype conversion that left the integer buffers alone
+        for new, old, name in ((qweight, self.qweight, "qweight"), (qzeros, self.qzeros, "qzeros"),
+                               (scales, self.scales, "scales")):
+            if new.shape != old.shape or new.dtype != old.dtype:
+                raise ValueError(f"{name}: moved tensor {tuple(new.shape)} {new.dtype} does not "
+                                 f"match {tuple(old.shape)} {old.dtype}")
+        if self.use_act and (perm.numel() != self.height or perm.dtype != torch.int32):
+            raise ValueError("perm must be int32 [K] for an act-order matrix")
+        devices = {qweight.device, qzeros.device, scales.device, perm.device}
+        if len(devices) != 1:
+            raise ValueError(f"packed tensors on several devices: {devices}")
+        had_dense = self.reconstructed_weight_float16 is not None
+        self.qweight, self.qzeros, self.scales = qweight, qzeros, scales
+        self.perm = perm
+        self.device = qweight.device
+        self.reconstructed_weight_float16 = None
+        if had_dense and self.device.type == "cuda":
+            self.reconstruct_weight()
+
+    def _check_resident(self) -> None:
+        if self.device.type != "cuda":
+            raise RuntimeError("Q4MatrixV2 is swapped out (its tensors are in host memory)")
 
     # -- configuration -------------------------------------------------------
     def set_tuning_params(self, tuning_params: TuningParams) -> None:
@@ -237,6 +310,7 @@ class Q4MatrixV2(object):
         product.  ``bias`` (fp16 [N]) is added after the fp16 rounding of
         the product, as ``output += bias`` does in the reference.
         """
+        self._check_resident()
         if x.device != self.device:
             raise ValueError(f"input on {x.device}, weights on {self.device}")
         if x.dtype not in (torch.float16, torch.bfloat16):
@@ -288,6 +362,7 @@ class Q4MatrixV2(object):
 
     def get_float16_weights_matrix_v2(self, out_matrix: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Dequantised fp16 weight [K, N] in the checkpoint's row order."""
+        self._check_resident()
         if out_matrix is None:
             out_matrix = torch.empty(self.height, self.width, dtype=torch.float16, device=self.device)
         if out_matrix.dtype != torch.float16 or tuple(out_matrix.shape[-2:]) != (self.height, self.width):

@@ -76,6 +76,14 @@ class MarlinQuantLinear(Linear):
         self.register_buffer("dequant_scale_column_map", q4_matrix.dequant_scale_column_map)
         self.q4_matrix = q4_matrix
 
+    def _apply(self, fn, recurse: bool = True):
+        """Module moves carry the repacked buffers; the matrix object is
+        re-pointed at the moved copies (no repack)."""
+        super()._apply(fn, recurse)
+        if self.q4_matrix is not None:
+            self.q4_matrix.rebind(**{name: getattr(self, name) for name in MarlinQ4Matrix._MOVED})
+        return self
+
     def _matrix(self) -> MarlinQ4Matrix:
         if self.q4_matrix is None:
             raise RuntimeError("MarlinQuantLinear must be repacked before use")

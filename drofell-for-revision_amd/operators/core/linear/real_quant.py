@@ -92,6 +92,21 @@ class QuantLinear(Linear):
         if flags.RECONSTRUCTE_WEIGTH_BFLOAT16:
             raise RuntimeError("bf16 reconstruction is not supported by the HIP backend")
 
+    def _apply(self, fn, recurse: bool = True):
+        """Module moves (swap-out to host memory, swap-in to a device) carry
+        the packed buffers; the matrix object is re-pointed at the moved
+        copies (no repack), and matrices with equal act-order permutations
+        share one device copy again."""
+        super()._apply(fn, recurse)
+        q4 = self.q4_matrix
+        if q4 is not None:
+            perm = self.perm
+            if q4.perm_group is not None:
+                perm = q4.perm_group.share(perm)
+                self._buffers["perm"] = perm
+            q4.rebind(self.qweight, self.qzeros, self.scales, perm)
+        return self
+
     def _matrix(self) -> Q4MatrixV2:
         if self.q4_matrix is None:
             raise RuntimeError("QuantLinear must be post_init()-ed (repacked) before use")
