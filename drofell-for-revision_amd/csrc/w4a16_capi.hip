@@ -293,6 +293,50 @@ int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
   return status_of(e);
 }
 
+int dw4_gemm_t_workspace_size(int m, int k, int n, int group_size, size_t* workspace_bytes) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (m < 0 || workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
+  *workspace_bytes = m == 0 ? 0 : dw4::gemm_t_ws_bytes(dw4::plan_gemm_t(m, k, n, cu_count()), m, k);
+  return DW4_OK;
+}
+
+int dw4_gemm_t(int m, int k, int n, int group_size, const uint16_t* g, int64_t ldg,
+               const int32_t* packed_qweight, const int32_t* packed_zeros,
+               const uint16_t* packed_scales, const int32_t* perm, uint16_t* out, int64_t ldo,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (m < 0) return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  if (!g || !packed_qweight || !packed_zeros || !packed_scales || !out) return DW4_ERR_INVALID_ARG;
+  if (ldg < n || ldo < k) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(g) || (ldg % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  const dw4::GemmTPlan plan = dw4::plan_gemm_t(m, k, n, cu_count());
+  float* part = nullptr;
+  if (plan.ns > 1) {
+    if (workspace == nullptr || workspace_bytes < dw4::gemm_t_ws_bytes(plan, m, k))
+      return DW4_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
+    part = static_cast<float*>(workspace);
+  }
+  dw4::GemmTArgs a;
+  a.M = m;
+  a.K = k;
+  a.N = n;
+  a.gs = group_size;
+  a.G = k / group_size;
+  a.g = g;
+  a.ldg = ldg;
+  a.pq = reinterpret_cast<const uint32_t*>(packed_qweight);
+  a.pz = reinterpret_cast<const uint32_t*>(packed_zeros);
+  a.ps = packed_scales;
+  a.perm = perm;
+  a.out = out;
+  a.ldo = ldo;
+  return status_of(dw4::launch_gemm_t(a, plan, part, static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

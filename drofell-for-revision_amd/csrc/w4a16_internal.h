@@ -183,4 +183,24 @@ hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t
                           const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,
                           int G, hipStream_t stream);
 
+// Transposed product out[M, K] = g[M, N] @ W^T (PEFT backward).
+struct GemmTArgs {
+  int M, K, N, gs, G;
+  const uint16_t* g;
+  int64_t ldg;
+  const uint32_t* pq;
+  const uint32_t* pz;
+  const uint16_t* ps;
+  const int32_t* perm;  // sorted row -> checkpoint row (act-order) or null
+  uint16_t* out;
+  int64_t ldo;
+};
+struct GemmTPlan {
+  int ns = 1;   // N-ranges (their fp32 partials are summed in order)
+  int spr = 0;  // strips per N-range
+};
+GemmTPlan plan_gemm_t(int m, int k, int n, int cus);
+size_t gemm_t_ws_bytes(const GemmTPlan& p, int m, int k);
+hipError_t launch_gemm_t(const GemmTArgs& a, const GemmTPlan& p, float* part, hipStream_t stream);
+
 }  // namespace dw4

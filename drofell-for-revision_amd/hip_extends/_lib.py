@@ -58,6 +58,10 @@ SIGNATURES = {
                                  _P, _c.c_size_t, _P]),
     "dw4_dequant": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
                                _c.c_int64, _P]),
+    "dw4_gemm_t": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64, _P, _P, _P,
+                              _P, _P, _c.c_int64, _P, _c.c_size_t, _P]),
+    "dw4_gemm_t_workspace_size": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                             _c.POINTER(_c.c_size_t)]),
     "dw4_gemm_group": (_c.c_int, [_c.c_int, _IP, _c.c_int, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_silu_mul": (_c.c_int, [_c.c_int, _P, _c.c_int64, _IP, _IP, _P, _c.c_int64,
                                      _P, _c.c_size_t, _P]),
@@ -71,7 +75,7 @@ SIGNATURES = {
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -135,4 +139,12 @@ def workspace_size(m: int, k: int, n: int, group_size: int, act_order: bool) -> 
     out = ctypes.c_size_t(0)
     check("dw4_workspace_size", lib.dw4_workspace_size(m, k, n, group_size, int(act_order),
                                                        ctypes.byref(out)))
+    return out.value
+
+
+def gemm_t_workspace_size(m: int, k: int, n: int, group_size: int) -> int:
+    lib = load()
+    out = ctypes.c_size_t(0)
+    check("dw4_gemm_t_workspace_size",
+          lib.dw4_gemm_t_workspace_size(m, k, n, group_size, ctypes.byref(out)))
     return out.value

@@ -47,6 +47,10 @@ class TuningParams:
     MAX_M: int = 4096
     # Prefill split-K factor; 0 lets the library choose from the tile count.
     PREFILL_SPLIT_K: int = 0
+    # Flattened M up to which the transposed product (PEFT backward) runs the
+    # packed kernel; above it the weight is dequantised and a dense GEMM runs,
+    # as in the reference.
+    TRANSPOSE_MAX_M: int = 128
 
 
 class CacheV2(object):
@@ -64,6 +68,7 @@ class CacheV2(object):
         self.temp_weight_size: int = 0
         self._workspace: Optional[torch.Tensor] = None
         self._temp_weight: Optional[torch.Tensor] = None
+        self._t_workspace: Optional[torch.Tensor] = None
         self.cache_created = False
 
     def update_workspace_size(self, nbytes: int) -> None:
@@ -89,6 +94,13 @@ class CacheV2(object):
         if not self.cache_created or self._workspace is None:
             raise RuntimeError("CacheV2.init_cache() must run before the first matmul")
         return self._workspace
+
+    def transpose_workspace(self, nbytes: int) -> torch.Tensor:
+        """fp32 partial planes of the transposed product, grown on demand
+        (the backward runs outside graph capture); no zero-fill needed."""
+        if self._t_workspace is None or self._t_workspace.numel() < nbytes:
+            self._t_workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+        return self._t_workspace
 
     @property
     def temp_weight(self) -> torch.Tensor:
@@ -351,6 +363,26 @@ class Q4MatrixV2(object):
         out = output.view(outshape)
         return out if in_dtype == torch.float16 else out.to(in_dtype)
 
+    def _transpose_native(self, x: torch.Tensor, output: Optional[torch.Tensor]) -> torch.Tensor:
+        if x.device != self.device:
+            raise ValueError(f"input on {x.device}, weights on {self.device}")
+        in_dtype = x.dtype
+        outshape = x.shape[:-1] + (self.height,)
+        g2 = _aligned_rows(x.reshape(-1, self.width).to(torch.float16))
+        m = g2.shape[0]
+        y = torch.empty((m, self.height), dtype=torch.float16, device=self.device)
+        nbytes = _lib.gemm_t_workspace_size(m, self.height, self.width, self.group_size)
+        ws = self.cache.transpose_workspace(nbytes)
+        _lib.call("dw4_gemm_t", m, self.height, self.width, self.group_size,
+                  g2.data_ptr(), g2.stride(0), self.qweight.data_ptr(), self.qzeros.data_ptr(),
+                  self.scales.data_ptr(), _ptr(self.perm) if self.use_act else None,
+                  y.data_ptr(), self.height, ws.data_ptr(), ws.numel(), _stream(self.device))
+        if output is not None:
+            output.view(m, self.height).copy_(y)
+            y = output
+        y = y.view(outshape)
+        return y if in_dtype == torch.float16 else y.to(in_dtype)
+
     def _dense_weight(self, temp_weight: Optional[torch.Tensor]) -> torch.Tensor:
         """The fp16 [K, N] weight dequantised into ``temp_weight`` (or the
         shared per-device buffer)."""
@@ -387,14 +419,21 @@ class Q4MatrixV2(object):
                          skip_reconstruct: bool = False) -> torch.Tensor:
         """``x @ W.T`` for x [..., N] (the activation gradient of the forward).
 
-        Same arguments as the reference (``exllama.py:528-544``): the weight
-        is the reconstructed one if present, else it is dequantised
-        bit-exactly into ``temp_weight`` (or the shared buffer) -- skipped
-        with ``skip_reconstruct`` when the caller already filled it -- and
-        the dense product is a plain library GEMM.
+        Same arguments as the reference (``exllama.py:528-544``).  With a
+        reconstructed weight, or ``skip_reconstruct`` (the caller already
+        filled ``temp_weight``), the product is the dense one over that
+        weight.  Otherwise, up to ``TuningParams.TRANSPOSE_MAX_M`` rows, the
+        packed kernel (``dw4_gemm_t``) reads the int4 words directly; above
+        it the weight is dequantised bit-exactly into ``temp_weight`` (or the
+        shared buffer) and a library GEMM runs, as in the reference.
         """
         if x.dtype not in (torch.float16, torch.bfloat16):
             raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
+        self._check_resident()
+        m = x.numel() // self.width
+        if self.reconstructed_weight_float16 is None and not skip_reconstruct \
+                and 0 < m <= self.tuning_params.TRANSPOSE_MAX_M:
+            return self._transpose_native(x, output)
         w = self.reconstructed_weight_float16
         if w is None:
             if skip_reconstruct:

@@ -16,6 +16,9 @@
  *                    Q4MatrixV2.matmul (cuda_extends/exllama.py:492-526)
  *   dw4_dequant      q4_to_half_matrix_v2 (entry.cpp:79-91) and
  *                    marlin_dequant_into (cuda_extends/marlin/marlin_dequant.cu:97-172)
+ *   dw4_gemm_t       q4_transpose_matmul_blas_v2 (entry.cpp:392-429 ->
+ *                    exllama/q4_transpose_matmul.cu:115-167), the PEFT backward
+ *                    of Q4MatrixV2.transpose_matmul (exllama.py:528-544)
  *   dw4_gemm_group   the q/k/v GEMMs of attention_forward_qkv_stage
  *                    (cuda_extends/exllama/fuse_v2/q_attn.cu:46-48) and the
  *                    gate/up GEMMs of mlp_forward (fuse_v2/q_mlp.cu:119-120)
@@ -85,7 +88,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 3
+#define DW4_ABI_VERSION 4
 
 enum {
   DW4_OK = 0,
@@ -158,6 +161,24 @@ int dw4_dequant(int k, int n, int group_size,
                 const int32_t* packed_qweight, const int32_t* packed_zeros,
                 const uint16_t* packed_scales, const int32_t* perm,
                 uint16_t* w, int64_t ldw, void* stream);
+
+/* out = g @ W^T, the activation gradient of y = x @ W (PEFT backward):
+ * g fp16 [m, n] (row stride ldg), out fp16 [m, k] (row stride ldo) in the
+ * checkpoint's row order (perm as given to dw4_repack).  The packed words
+ * are read once; the weight entering the fp32-accumulated products is the
+ * exact fp16(s * (q - z)) that dw4_dequant writes, so the result is the dense
+ * product with dw4_dequant's output up to the order of fp32 sums.
+ * g 16-byte aligned with ldg % 8 == 0; ldo >= k.  workspace: at least
+ * dw4_gemm_t_workspace_size bytes (no zero-fill needed; 0 bytes for some
+ * shapes).  Never synchronises or allocates.  Replaces
+ * q4_transpose_matmul_blas_v2 (entry.cpp:392-429 ->
+ * q4_transpose_matmul.cu:115-167: dequantise to fp16 K x N, then a dense
+ * GEMM). */
+int dw4_gemm_t(int m, int k, int n, int group_size, const uint16_t* g, int64_t ldg,
+               const int32_t* packed_qweight, const int32_t* packed_zeros,
+               const uint16_t* packed_scales, const int32_t* perm, uint16_t* out, int64_t ldo,
+               void* workspace, size_t workspace_bytes, void* stream);
+int dw4_gemm_t_workspace_size(int m, int k, int n, int group_size, size_t* workspace_bytes);
 
 /* ---------------------------------------------------------------------------
  * Decoder-stage calls: several projections of one layer per launch.
