@@ -78,6 +78,7 @@ class MarlinDenseCache:
         self.workspace_bytes = 0
         self._temp_weight: Optional[torch.Tensor] = None
         self._workspace: Optional[torch.Tensor] = None
+        self._t_workspace: Optional[torch.Tensor] = None
 
     def update(self, in_features: int, out_features: int, workspace_bytes: int = 0) -> None:
         if self._temp_weight is not None:
@@ -101,6 +102,12 @@ class MarlinDenseCache:
         if elements > self._temp_weight.numel():
             raise RuntimeError("Marlin dense cache is too small")
         return self._temp_weight[:elements].view(in_features, out_features)
+
+    def transpose_workspace(self, nbytes: int) -> torch.Tensor:
+        """fp32 partial planes of the packed transposed product, grown on demand."""
+        if self._t_workspace is None or self._t_workspace.numel() < nbytes:
+            self._t_workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+        return self._t_workspace
 
     @property
     def workspace(self) -> torch.Tensor:
@@ -255,8 +262,30 @@ class MarlinQ4Matrix:
             self.reconstruct_weight(weight)
         return self.dense_matmul(x, weight), weight if cache_weight else None
 
+    # flattened rows up to which the activation gradient reads the packed
+    # words directly (dw4_gemm_t) instead of a reconstructed dense weight
+    TRANSPOSE_MAX_M = 128
+
     def transpose_matmul(self, x: torch.Tensor,
                          weight: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``x @ W.T`` for x [..., N]: with ``weight`` (a reconstructed fp16
+        [K, N]) the dense product; otherwise, up to ``TRANSPOSE_MAX_M`` rows,
+        the packed kernel, above it reconstruct-then-dense as the reference
+        (``marlin.py:355-396``)."""
+        self._check_resident()
+        m = x.numel() // self.out_features
+        if weight is None and 0 < m <= self.TRANSPOSE_MAX_M:
+            g2 = _aligned_rows(x.reshape(-1, self.out_features).to(torch.float16))
+            out = torch.empty((m, self.in_features), dtype=torch.float16, device=x.device)
+            nbytes = _lib.gemm_t_workspace_size(m, self.in_features, self.out_features,
+                                                self.group_size)
+            ws = self.cache.transpose_workspace(nbytes)
+            _lib.call("dw4_gemm_t", m, self.in_features, self.out_features, self.group_size,
+                      g2.data_ptr(), g2.stride(0), self.qweight.data_ptr(),
+                      self.qzeros.data_ptr(), self.scales.data_ptr(), _ptr(self._perm),
+                      out.data_ptr(), self.in_features, ws.data_ptr(), ws.numel(),
+                      _stream(x.device))
+            return out.reshape(*x.shape[:-1], self.in_features)
         if weight is None:
             weight = self.cache.weight(self.in_features, self.out_features)
             self.reconstruct_weight(weight)

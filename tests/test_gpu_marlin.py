@@ -111,10 +111,12 @@ def test_marlin_merge_qkv_act_order(hip_device):
         y = merged(x.to(hip_device))
         torch.cuda.synchronize()
         check_tol(y, gptq.gemm_ref(x.numpy(), wcat), f"merged M={m}")
-    say("marlin merged input gradient")
-    xg = make_x(16, k, seed=7).to(hip_device).requires_grad_(True)
-    yg = merged(xg)
-    gout = make_x(16, 3 * n, seed=8)
-    yg.backward(gout.to(hip_device))
-    torch.cuda.synchronize()
-    check_tol(xg.grad, gout.numpy().astype(np.float64) @ wcat.astype(np.float64).T, "grad")
+    for m in (16, 200):  # packed transposed kernel, then reconstruct + dense
+        say(f"marlin merged input gradient M={m}")
+        xg = make_x(m, k, seed=7).to(hip_device).requires_grad_(True)
+        yg = merged(xg)
+        gout = make_x(m, 3 * n, seed=8)
+        yg.backward(gout.to(hip_device))
+        torch.cuda.synchronize()
+        check_tol(xg.grad, gout.numpy().astype(np.float64) @ wcat.astype(np.float64).T,
+                  f"grad M={m}")
