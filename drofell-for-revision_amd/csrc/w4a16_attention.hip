@@ -1,0 +1,370 @@
+// Paged-attention decode and the KV-cache slot operations of the decoder
+// stage.
+//
+// Cache layout (the reference's, operators/core/block/common.py:7-60 and
+// cuda_extends/vllm/cache_kernels.cu:242-285, in
+// /root/reference/After-Revision-DROFELL): the cache is a set of blocks of
+// BS token slots; each block has a key part [kv_heads][head_size/8][BS][8]
+// and a value part [kv_heads][head_size][BS] (fp16), reached through
+// per-block pointer tables, with kv_head_stride elements between the heads
+// of a block.  A token's slot s lives in block s / BS at offset s % BS.
+//
+// paged_attention_kernel: one workgroup per (sequence, kv head, context
+// partition).  It serves every query head of the kv head's group
+// (head h uses kv head h / (heads / kv_heads)), so each K and V byte is
+// read once per group.  Per partition of up to 512 tokens:
+//   logits (fp32, LDS) = scale * q . k (+ alibi slope * (t - ctx + 1));
+//   p = exp(logit - max); out = sum p v / sum p.
+// Waves take the partition's blocks round-robin.  For q . k a lane holds one
+// token and a slice of 8 dims (one 16-byte load); lanes of one token meet
+// through cross-lane adds.  For p . v a lane holds whole dims (a row of BS
+// tokens).  Partitions write their max, sum and unnormalised fp32 output;
+// a second kernel combines them in partition order (deterministic).  With a
+// single partition the first kernel writes the output directly.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+
+#include "w4a16_device.h"
+#include "w4a16_internal.h"
+
+namespace dw4 {
+
+namespace {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// Block-wide reduction in a fixed order (waves' results summed 0..3).
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = MAX ? wave_max(v) : wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
+  return r;
+}
+
+template <int HS, int BS, int GMAX>
+__global__ void __launch_bounds__(kAttnThreads)
+paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
+                       uint16_t* __restrict__ out, int64_t o_stride,
+                       const int64_t* __restrict__ kptr, const int64_t* __restrict__ vptr,
+                       int kv_head_stride, int num_heads, int num_kv_heads, float scale,
+                       const int32_t* __restrict__ block_tables, int max_blocks,
+                       const int32_t* __restrict__ context_lens,
+                       const float* __restrict__ alibi, int part_tokens, int num_parts,
+                       float* __restrict__ ws_ml, float* __restrict__ ws_out) {
+  constexpr int SLICES = HS / 8;         // 16-byte slices of a key row
+  constexpr int TPL = 64 / BS;           // slice groups per wave (lanes of one token)
+  constexpr int SPL = SLICES / TPL;      // slices per lane
+  constexpr int DPL = HS / 64;           // value dims per lane
+  static_assert(HS % 64 == 0 && 64 % BS == 0 && SLICES % TPL == 0, "shape");
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int G = num_heads / num_kv_heads;  // query heads per kv head (<= GMAX)
+  float* qs = sm;                           // [G][HS] fp32 query (scaled)
+  float* logit = qs + GMAX * HS;            // [G][part_tokens]
+  float* red = logit + GMAX * part_tokens;  // [waves][G][HS] partial outputs
+  float* scratch = red + kAttnWaves * GMAX * HS;  // 8 floats
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int seq = blockIdx.x / num_kv_heads;
+  const int kvh = blockIdx.x % num_kv_heads;
+  const int part = blockIdx.y;
+  const int h0 = kvh * G;
+  // a context longer than the block table is cut to it (never read past a row)
+  const int ctx = min(context_lens[seq], max_blocks * BS);
+  const int t0 = part * part_tokens;
+  const int t1 = min(ctx, t0 + part_tokens);
+  const int nt = t1 - t0;
+  const bool direct = num_parts == 1;
+  if (nt <= 0) {  // partition past this sequence's context: an empty partial
+    if (!direct && tid < G) {
+      const size_t r = ((size_t)seq * num_heads + h0 + tid) * num_parts + part;
+      ws_ml[2 * r] = -FLT_MAX;
+      ws_ml[2 * r + 1] = 0.f;
+    }
+    return;
+  }
+  for (int i = tid; i < G * HS; i += kAttnThreads) {
+    const int g = i / HS, d = i % HS;
+    qs[i] = scale * (float)as_h(query[(size_t)seq * q_stride + (size_t)(h0 + g) * HS + d]);
+  }
+  __syncthreads();
+
+  const int32_t* btab = block_tables + (size_t)seq * max_blocks + t0 / BS;
+  const int nb = (nt + BS - 1) / BS;
+  const int tt = lane % BS;   // token of this lane within a block
+  const int sg = lane / BS;   // slice group
+  // q . k
+  for (int b = wave; b < nb; b += kAttnWaves) {
+    const uint16_t* kb = reinterpret_cast<const uint16_t*>(kptr[btab[b]]) +
+                         (size_t)kvh * kv_head_stride;
+    h8 kv[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) kv[j] = *(const h8*)(kb + ((sg + TPL * j) * BS + tt) * 8);
+    float dot[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      dot[g] = 0.f;
+      if (g < G) {
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+          const float* qv = qs + g * HS + (sg + TPL * j) * 8;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dot[g] = fmaf(qv[e], (float)kv[j][e], dot[g]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+#pragma unroll
+      for (int off = BS; off < 64; off <<= 1) dot[g] += __shfl_xor(dot[g], off);
+    }
+    const int t = t0 + b * BS + tt;
+    if (sg == 0) {
+#pragma unroll
+      for (int g = 0; g < GMAX; ++g) {
+        if (g < G) {
+          float l = dot[g];
+          if (alibi != nullptr) l += alibi[h0 + g] * (float)(t - ctx + 1);
+          logit[g * part_tokens + b * BS + tt] = t < t1 ? l : -FLT_MAX;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // softmax numerators and their sums, per query head
+  float mx[GMAX], sum[GMAX];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    mx[g] = -FLT_MAX;
+    sum[g] = 0.f;
+    if (g < G) {
+      float m = -FLT_MAX;
+      for (int t = tid; t < nt; t += kAttnThreads) m = fmaxf(m, logit[g * part_tokens + t]);
+      mx[g] = block_reduce<true>(m, scratch);
+      float s = 0.f;
+      for (int t = tid; t < nb * BS; t += kAttnThreads) {
+        const float p = t < nt ? __expf(logit[g * part_tokens + t] - mx[g]) : 0.f;
+        logit[g * part_tokens + t] = p;
+        s += p;
+      }
+      sum[g] = block_reduce<false>(s, scratch);
+    }
+  }
+  __syncthreads();
+
+  // p . v: lane holds dims lane + 64 j for every query head of the group
+  float acc[GMAX][DPL];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
+  for (int b = wave; b < nb; b += kAttnWaves) {
+    const uint16_t* vb = reinterpret_cast<const uint16_t*>(vptr[btab[b]]) +
+                         (size_t)kvh * kv_head_stride;
+    const int valid = min(BS, nt - b * BS);  // tokens of this block in the context
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const uint16_t* row = vb + (size_t)(lane + 64 * j) * BS;
+#pragma unroll
+      for (int u = 0; u < BS / 8; ++u) {
+        const h8 v = *(const h8*)(row + 8 * u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tb = 8 * u + e;
+          // slots past the context may hold anything: never multiply them
+          const float vf = tb < valid ? (float)v[e] : 0.f;
+#pragma unroll
+          for (int g = 0; g < GMAX; ++g)
+            if (g < G) acc[g][j] = fmaf(logit[g * part_tokens + b * BS + tb], vf, acc[g][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+      if (g < G) red[(wave * GMAX + g) * HS + lane + 64 * j] = acc[g][j];
+  __syncthreads();
+  for (int i = tid; i < G * HS; i += kAttnThreads) {
+    const int g = i / HS, d = i % HS;
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) o += red[(w * GMAX + g) * HS + d];
+    float s = 0.f, m = 0.f;
+#pragma unroll
+    for (int gg = 0; gg < GMAX; ++gg)
+      if (gg == g) { s = sum[gg]; m = mx[gg]; }
+    if (direct) {
+      out[(size_t)seq * o_stride + (size_t)(h0 + g) * HS + d] = h_bits((_Float16)(o / s));
+    } else {
+      const size_t r = ((size_t)seq * num_heads + h0 + g) * num_parts + part;
+      ws_out[r * HS + d] = o;
+      if (d == 0) {
+        ws_ml[2 * r] = m;
+        ws_ml[2 * r + 1] = s;
+      }
+    }
+  }
+}
+
+// Combine the partitions of one (sequence, head) in partition order.
+template <int HS>
+__global__ void __launch_bounds__(HS)
+paged_attention_reduce_kernel(uint16_t* __restrict__ out, int64_t o_stride, int num_heads,
+                              const int32_t* __restrict__ context_lens, int max_tokens,
+                              int part_tokens,
+                              int num_parts, const float* __restrict__ ws_ml,
+                              const float* __restrict__ ws_out) {
+  const int seq = blockIdx.x / num_heads, h = blockIdx.x % num_heads;
+  const int d = threadIdx.x;
+  const int ctx = min(context_lens[seq], max_tokens);
+  const int parts = min(num_parts, (ctx + part_tokens - 1) / part_tokens);
+  const size_t r0 = ((size_t)seq * num_heads + h) * num_parts;
+  float gmax = -FLT_MAX;
+  for (int p = 0; p < parts; ++p) gmax = fmaxf(gmax, ws_ml[2 * (r0 + p)]);
+  float total = 0.f, o = 0.f;
+  for (int p = 0; p < parts; ++p) {
+    const float w = __expf(ws_ml[2 * (r0 + p)] - gmax);
+    total += ws_ml[2 * (r0 + p) + 1] * w;
+    o += ws_out[(r0 + p) * HS + d] * w;
+  }
+  out[(size_t)seq * o_stride + (size_t)h * HS + d] = h_bits((_Float16)(o / total));
+}
+
+// One workgroup per token: its key and value rows go to their slot.
+// restore: the reverse copy (slots to the token-major tensors).
+__global__ void reshape_and_cache_kernel(uint16_t* __restrict__ key, int64_t key_stride,
+                                         uint16_t* __restrict__ value, int64_t value_stride,
+                                         const int64_t* __restrict__ kptr,
+                                         const int64_t* __restrict__ vptr,
+                                         const int64_t* __restrict__ slots, int num_kv_heads,
+                                         int head_size, int block_size, int kv_head_stride,
+                                         bool restore) {
+  const int64_t tok = blockIdx.x;
+  const int64_t slot = slots[tok];
+  if (slot < 0) return;  // padding token
+  const int64_t blk = slot / block_size;
+  const int off = (int)(slot % block_size);
+  uint16_t* kc = reinterpret_cast<uint16_t*>(kptr[blk]);
+  uint16_t* vc = reinterpret_cast<uint16_t*>(vptr[blk]);
+  const int n = num_kv_heads * head_size;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int h = i / head_size, d = i % head_size;
+    const size_t kt = (size_t)h * kv_head_stride + ((size_t)(d / 8) * block_size + off) * 8 + d % 8;
+    const size_t vt = (size_t)h * kv_head_stride + (size_t)d * block_size + off;
+    if (restore) {
+      key[tok * key_stride + i] = kc[kt];
+      value[tok * value_stride + i] = vc[vt];
+    } else {
+      kc[kt] = key[tok * key_stride + i];
+      vc[vt] = value[tok * value_stride + i];
+    }
+  }
+}
+
+template <int HS, int BS, int GMAX>
+hipError_t launch_pa(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                     hipStream_t stream) {
+  const size_t smem = sizeof(float) * ((size_t)GMAX * HS + (size_t)GMAX * p.part_tokens +
+                                       (size_t)kAttnWaves * GMAX * HS + 8);
+  const dim3 grid((unsigned)(a.num_seqs * a.num_kv_heads), (unsigned)p.num_parts);
+  float* ws_ml = p.num_parts > 1 ? ws : nullptr;
+  float* ws_out = p.num_parts > 1 ? ws + 2 * (size_t)a.num_seqs * a.num_heads * p.num_parts : nullptr;
+  paged_attention_kernel<HS, BS, GMAX><<<grid, kAttnThreads, smem, stream>>>(
+      a.query, a.q_stride, a.out, a.o_stride, a.kptr, a.vptr, a.kv_head_stride, a.num_heads,
+      a.num_kv_heads, a.scale, a.block_tables, a.max_blocks, a.context_lens, a.alibi,
+      p.part_tokens, p.num_parts, ws_ml, ws_out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.num_parts == 1) return e;
+  paged_attention_reduce_kernel<HS><<<(unsigned)(a.num_seqs * a.num_heads), HS, 0, stream>>>(
+      a.out, a.o_stride, a.num_heads, a.context_lens, a.max_blocks * BS, p.part_tokens,
+      p.num_parts, ws_ml, ws_out);
+  return hipGetLastError();
+}
+
+template <int HS, int BS>
+hipError_t launch_pa_g(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                       hipStream_t stream) {
+  const int g = a.num_heads / a.num_kv_heads;
+  if (g == 1) return launch_pa<HS, BS, 1>(a, p, ws, stream);
+  if (g <= 4) return launch_pa<HS, BS, 4>(a, p, ws, stream);
+  return launch_pa<HS, BS, 8>(a, p, ws, stream);
+}
+
+template <int HS>
+hipError_t launch_pa_bs(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                        hipStream_t stream) {
+  if (a.block_size == 16) return launch_pa_g<HS, 16>(a, p, ws, stream);
+  return launch_pa_g<HS, 32>(a, p, ws, stream);
+}
+
+}  // namespace
+
+PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_size,
+                                   int max_context_len, int cus) {
+  PagedAttnPlan p;
+  const int blocks = std::max(1, (max_context_len + block_size - 1) / block_size);
+  // about four workgroups per CU; partitions of whole blocks, at most 512 tokens
+  const int pairs = std::max(1, num_seqs * num_kv_heads);
+  int parts = std::max(1, (4 * cus + pairs - 1) / pairs);
+  parts = std::min(parts, blocks);
+  int bpp = (blocks + parts - 1) / parts;
+  bpp = std::min(bpp, kAttnMaxPartTokens / block_size);
+  p.part_tokens = bpp * block_size;
+  p.num_parts = (blocks + bpp - 1) / bpp;
+  return p;
+}
+
+size_t paged_attention_ws_bytes(const PagedAttnPlan& p, int num_seqs, int num_heads,
+                                int head_size) {
+  if (p.num_parts <= 1) return 0;
+  return sizeof(float) * (size_t)num_seqs * num_heads * p.num_parts * (2 + (size_t)head_size);
+}
+
+hipError_t launch_paged_attention(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                                  hipStream_t stream) {
+  switch (a.head_size) {
+    case 64: return launch_pa_bs<64>(a, p, ws, stream);
+    case 128: return launch_pa_bs<128>(a, p, ws, stream);
+    case 256: return launch_pa_bs<256>(a, p, ws, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_reshape_and_cache(uint16_t* key, int64_t key_stride, uint16_t* value,
+                                    int64_t value_stride, const int64_t* kptr, const int64_t* vptr,
+                                    const int64_t* slots, int num_tokens, int num_kv_heads,
+                                    int head_size, int block_size, int kv_head_stride,
+                                    bool restore, hipStream_t stream) {
+  const int n = num_kv_heads * head_size;
+  reshape_and_cache_kernel<<<(unsigned)num_tokens, std::min(1024, n), 0, stream>>>(
+      key, key_stride, value, value_stride, kptr, vptr, slots, num_kv_heads, head_size,
+      block_size, kv_head_stride, restore);
+  return hipGetLastError();
+}
+
+}  // namespace dw4

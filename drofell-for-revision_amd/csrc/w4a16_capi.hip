@@ -293,6 +293,121 @@ int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
   return status_of(e);
 }
 
+static int check_cache_args(int num_tokens, int num_kv_heads, int head_size, int block_size,
+                            const void* key, int64_t key_stride, const void* value,
+                            int64_t value_stride, const int64_t* kp, const int64_t* vp,
+                            int kv_head_stride, const int64_t* slots) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0) return DW4_ERR_INVALID_ARG;
+  if (head_size % 8 != 0 || (block_size != 16 && block_size != 32)) return DW4_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return DW4_OK;
+  if (!key || !value || !kp || !vp || !slots) return DW4_ERR_INVALID_ARG;
+  const int64_t row = (int64_t)num_kv_heads * head_size;
+  if (key_stride < row || value_stride < row || kv_head_stride < block_size * head_size)
+    return DW4_ERR_INVALID_ARG;
+  return DW4_OK;
+}
+
+int dw4_reshape_and_cache(int num_tokens, int num_kv_heads, int head_size, int block_size,
+                          const uint16_t* key, int64_t key_stride, const uint16_t* value,
+                          int64_t value_stride, const int64_t* key_block_ptrs,
+                          const int64_t* value_block_ptrs, int kv_head_stride,
+                          const int64_t* slot_mapping, void* stream) {
+  const int st = check_cache_args(num_tokens, num_kv_heads, head_size, block_size, key, key_stride,
+                                  value, value_stride, key_block_ptrs, value_block_ptrs,
+                                  kv_head_stride, slot_mapping);
+  if (st != DW4_OK || num_tokens == 0) return st;
+  return status_of(dw4::launch_reshape_and_cache(
+      const_cast<uint16_t*>(key), key_stride, const_cast<uint16_t*>(value), value_stride,
+      key_block_ptrs, value_block_ptrs, slot_mapping, num_tokens, num_kv_heads, head_size,
+      block_size, kv_head_stride, false, static_cast<hipStream_t>(stream)));
+}
+
+int dw4_restore_from_cache(int num_tokens, int num_kv_heads, int head_size, int block_size,
+                           uint16_t* key, int64_t key_stride, uint16_t* value,
+                           int64_t value_stride, const int64_t* key_block_ptrs,
+                           const int64_t* value_block_ptrs, int kv_head_stride,
+                           const int64_t* slot_mapping, void* stream) {
+  const int st = check_cache_args(num_tokens, num_kv_heads, head_size, block_size, key, key_stride,
+                                  value, value_stride, key_block_ptrs, value_block_ptrs,
+                                  kv_head_stride, slot_mapping);
+  if (st != DW4_OK || num_tokens == 0) return st;
+  return status_of(dw4::launch_reshape_and_cache(
+      key, key_stride, value, value_stride, key_block_ptrs, value_block_ptrs, slot_mapping,
+      num_tokens, num_kv_heads, head_size, block_size, kv_head_stride, true,
+      static_cast<hipStream_t>(stream)));
+}
+
+static int check_attn_shape(int num_seqs, int num_heads, int num_kv_heads, int head_size,
+                            int block_size, int max_context_len) {
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_context_len < 0)
+    return DW4_ERR_INVALID_ARG;
+  if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > dw4::kAttnMaxGroup)
+    return DW4_ERR_UNSUPPORTED;
+  if ((head_size != 64 && head_size != 128 && head_size != 256) ||
+      (block_size != 16 && block_size != 32))
+    return DW4_ERR_UNSUPPORTED;
+  return DW4_OK;
+}
+
+int dw4_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
+                                       int head_size, int block_size, int max_context_len,
+                                       size_t* workspace_bytes) {
+  const int st = check_attn_shape(num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                                  max_context_len);
+  if (st != DW4_OK) return st;
+  if (workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
+  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_kv_heads, block_size,
+                                                         max_context_len, cu_count());
+  *workspace_bytes = num_seqs == 0 ? 0 : dw4::paged_attention_ws_bytes(p, num_seqs, num_heads, head_size);
+  return DW4_OK;
+}
+
+int dw4_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_size,
+                        int block_size, const uint16_t* query, int64_t q_stride, uint16_t* out,
+                        int64_t o_stride, const int64_t* key_block_ptrs,
+                        const int64_t* value_block_ptrs, int kv_head_stride, float scale,
+                        const int32_t* block_tables, int max_blocks_per_seq,
+                        const int32_t* context_lens, int max_context_len,
+                        const float* alibi_slopes, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  int st = check_attn_shape(num_seqs, num_heads, num_kv_heads, head_size, block_size,
+                            max_context_len);
+  if (st != DW4_OK) return st;
+  if (num_seqs == 0) return DW4_OK;
+  if (!query || !out || !key_block_ptrs || !value_block_ptrs || !block_tables || !context_lens)
+    return DW4_ERR_INVALID_ARG;
+  const int64_t row = (int64_t)num_heads * head_size;
+  if (q_stride < row || o_stride < row || kv_head_stride < block_size * head_size ||
+      max_context_len < 1 || max_blocks_per_seq * block_size < max_context_len)
+    return DW4_ERR_INVALID_ARG;
+  if (!aligned16(query) || q_stride % 8 != 0) return DW4_ERR_MISALIGNED;
+  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_kv_heads, block_size,
+                                                         max_context_len, cu_count());
+  const size_t need = dw4::paged_attention_ws_bytes(p, num_seqs, num_heads, head_size);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return DW4_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(workspace)) return DW4_ERR_MISALIGNED;
+  dw4::PagedAttnArgs a;
+  a.num_seqs = num_seqs;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.head_size = head_size;
+  a.block_size = block_size;
+  a.query = query;
+  a.q_stride = q_stride;
+  a.out = out;
+  a.o_stride = o_stride;
+  a.kptr = key_block_ptrs;
+  a.vptr = value_block_ptrs;
+  a.kv_head_stride = kv_head_stride;
+  a.scale = scale;
+  a.block_tables = block_tables;
+  a.max_blocks = max_blocks_per_seq;
+  a.context_lens = context_lens;
+  a.alibi = alibi_slopes;
+  return status_of(dw4::launch_paged_attention(a, p, static_cast<float*>(workspace),
+                                               static_cast<hipStream_t>(stream)));
+}
+
 int dw4_gemm_t_workspace_size(int m, int k, int n, int group_size, size_t* workspace_bytes) {
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;

@@ -203,4 +203,39 @@ GemmTPlan plan_gemm_t(int m, int k, int n, int cus);
 size_t gemm_t_ws_bytes(const GemmTPlan& p, int m, int k);
 hipError_t launch_gemm_t(const GemmTArgs& a, const GemmTPlan& p, float* part, hipStream_t stream);
 
+// Paged-attention decode over the block pointer tables of a KV cache.
+constexpr int kAttnMaxPartTokens = 512;  // tokens per context partition, at most
+constexpr int kAttnMaxGroup = 8;         // query heads per kv head, at most
+struct PagedAttnArgs {
+  int num_seqs, num_heads, num_kv_heads, head_size, block_size;
+  const uint16_t* query;  // [num_seqs][num_heads][head_size], q_stride per sequence
+  int64_t q_stride;
+  uint16_t* out;          // same shape, o_stride per sequence
+  int64_t o_stride;
+  const int64_t* kptr;    // per-block key / value base addresses
+  const int64_t* vptr;
+  int kv_head_stride;     // elements between kv heads within a block
+  float scale;
+  const int32_t* block_tables;  // [num_seqs][max_blocks]
+  int max_blocks;
+  const int32_t* context_lens;  // [num_seqs], each >= 1
+  const float* alibi;           // [num_heads] or null
+};
+struct PagedAttnPlan {
+  int part_tokens = kAttnMaxPartTokens;
+  int num_parts = 1;
+};
+PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_size,
+                                   int max_context_len, int cus);
+size_t paged_attention_ws_bytes(const PagedAttnPlan& p, int num_seqs, int num_heads,
+                                int head_size);
+hipError_t launch_paged_attention(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                                  hipStream_t stream);
+// Token rows to their cache slots (restore: slots back to rows); slot < 0 skips a row.
+hipError_t launch_reshape_and_cache(uint16_t* key, int64_t key_stride, uint16_t* value,
+                                    int64_t value_stride, const int64_t* kptr, const int64_t* vptr,
+                                    const int64_t* slots, int num_tokens, int num_kv_heads,
+                                    int head_size, int block_size, int kv_head_stride,
+                                    bool restore, hipStream_t stream);
+
 }  // namespace dw4

@@ -62,6 +62,16 @@ SIGNATURES = {
                               _P, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_t_workspace_size": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                              _c.POINTER(_c.c_size_t)]),
+    "dw4_reshape_and_cache": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64,
+                                         _P, _c.c_int64, _P, _P, _c.c_int, _P, _P]),
+    "dw4_restore_from_cache": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64,
+                                          _P, _c.c_int64, _P, _P, _c.c_int, _P, _P]),
+    "dw4_paged_attention": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _P,
+                                       _c.c_int64, _P, _c.c_int64, _P, _P, _c.c_int, _c.c_float,
+                                       _P, _c.c_int, _P, _c.c_int, _P, _P, _c.c_size_t, _P]),
+    "dw4_paged_attention_workspace_size": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int,
+                                                      _c.c_int, _c.c_int,
+                                                      _c.POINTER(_c.c_size_t)]),
     "dw4_gemm_group": (_c.c_int, [_c.c_int, _IP, _c.c_int, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_silu_mul": (_c.c_int, [_c.c_int, _P, _c.c_int64, _IP, _IP, _P, _c.c_int64,
                                      _P, _c.c_size_t, _P]),
@@ -75,7 +85,7 @@ SIGNATURES = {
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
@@ -147,4 +157,14 @@ def gemm_t_workspace_size(m: int, k: int, n: int, group_size: int) -> int:
     out = ctypes.c_size_t(0)
     check("dw4_gemm_t_workspace_size",
           lib.dw4_gemm_t_workspace_size(m, k, n, group_size, ctypes.byref(out)))
+    return out.value
+
+
+def paged_attention_workspace_size(num_seqs: int, num_heads: int, num_kv_heads: int,
+                                   head_size: int, block_size: int, max_context_len: int) -> int:
+    lib = load()
+    out = ctypes.c_size_t(0)
+    check("dw4_paged_attention_workspace_size", lib.dw4_paged_attention_workspace_size(
+        num_seqs, num_heads, num_kv_heads, head_size, block_size, max_context_len,
+        ctypes.byref(out)))
     return out.value

@@ -11,3 +11,5 @@ RECONSTRUCTE_WEIGTH_FLOAT16 = False
 RECONSTRUCTE_WEIGTH_BFLOAT16 = False
 # In training, keep the forward's dequantised weight for the backward.
 REUSE_RECONSTRUCT_CACHE_WHEN_GRAD = True
+# Token slots per KV-cache block (the reference's operators/flags.py:28-29).
+BLOCK_SIZE = 32

@@ -16,6 +16,13 @@
  *                    Q4MatrixV2.matmul (cuda_extends/exllama.py:492-526)
  *   dw4_dequant      q4_to_half_matrix_v2 (entry.cpp:79-91) and
  *                    marlin_dequant_into (cuda_extends/marlin/marlin_dequant.cu:97-172)
+ *   dw4_reshape_and_cache / dw4_restore_from_cache / dw4_paged_attention
+ *                    reshape_and_cache, restore_from_cache
+ *                    (cuda_extends/vllm/cache_kernels.cu:242-420) and
+ *                    paged_attention_v1 / v2
+ *                    (cuda_extends/vllm/attention/attention_kernels.cu:1602-1843)
+ *                    as operators/core/attention/real_page.py:23-189 and
+ *                    operators/core/block/real.py:66-106 call them
  *   dw4_gemm_t       q4_transpose_matmul_blas_v2 (entry.cpp:392-429 ->
  *                    exllama/q4_transpose_matmul.cu:115-167), the PEFT backward
  *                    of Q4MatrixV2.transpose_matmul (exllama.py:528-544)
@@ -88,7 +95,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 4
+#define DW4_ABI_VERSION 5
 
 enum {
   DW4_OK = 0,
@@ -256,6 +263,63 @@ int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint
                             uint16_t* rms, int64_t ldr, const dw4_item* gate, const dw4_item* up,
                             const dw4_item* down, void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged KV cache and decode attention (the stage's other HBM stream).
+ *
+ * Cache layout: blocks of block_size (16 or 32) token slots; per block a key
+ * part [kv_heads][head_size/8][block_size][8] and a value part
+ * [kv_heads][head_size][block_size] (fp16), at the addresses in the
+ * int64 tables key_block_ptrs / value_block_ptrs (device memory, one entry
+ * per block), kv_head_stride elements between the kv heads of a block.
+ * Slot s is offset s % block_size of block s / block_size.
+ * ------------------------------------------------------------------------- */
+
+/* key, value fp16 [num_tokens][num_kv_heads][head_size] (row strides
+ * key_stride, value_stride) to the slots in slot_mapping (int64 device
+ * [num_tokens]; negative = padding, skipped).  Replaces reshape_and_cache
+ * (cuda_extends/vllm/cache_kernels.cu:242-285, :287-330). */
+int dw4_reshape_and_cache(int num_tokens, int num_kv_heads, int head_size, int block_size,
+                          const uint16_t* key, int64_t key_stride, const uint16_t* value,
+                          int64_t value_stride, const int64_t* key_block_ptrs,
+                          const int64_t* value_block_ptrs, int kv_head_stride,
+                          const int64_t* slot_mapping, void* stream);
+
+/* The reverse copy: slots back to token rows.  Replaces restore_from_cache
+ * (cache_kernels.cu:332-420). */
+int dw4_restore_from_cache(int num_tokens, int num_kv_heads, int head_size, int block_size,
+                           uint16_t* key, int64_t key_stride, uint16_t* value,
+                           int64_t value_stride, const int64_t* key_block_ptrs,
+                           const int64_t* value_block_ptrs, int kv_head_stride,
+                           const int64_t* slot_mapping, void* stream);
+
+/* Decode attention of one new token per sequence over its cached context:
+ * out[s][h] = softmax_t(scale * q[s][h] . k_t (+ alibi[h] * (t - ctx + 1)))
+ * . v_t for t < context_lens[s], with query head h reading kv head
+ * h / (num_heads / num_kv_heads) (the reference's head_mapping,
+ * repeat_interleave(arange(kv_heads), groups)).  query, out fp16
+ * [num_seqs][num_heads][head_size] with row strides q_stride, o_stride per
+ * sequence; block_tables int32 [num_seqs][max_blocks_per_seq];
+ * context_lens int32 [num_seqs], each in 1..max_context_len; alibi_slopes
+ * float [num_heads] or NULL.  head_size 64, 128 or 256; num_heads a
+ * multiple of num_kv_heads with at most 8 query heads per kv head.
+ * Softmax and both products in fp32; long contexts are split into
+ * partitions combined in a fixed order (deterministic).  workspace: at
+ * least dw4_paged_attention_workspace_size bytes (0 for short contexts).
+ * Never synchronises or allocates.  Replaces paged_attention_v1 / v2
+ * (cuda_extends/vllm/attention/attention_kernels.cu:1602-1632, 1786-1843)
+ * as operators/core/attention/real_page.py:23-189 calls them. */
+int dw4_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_size,
+                        int block_size, const uint16_t* query, int64_t q_stride, uint16_t* out,
+                        int64_t o_stride, const int64_t* key_block_ptrs,
+                        const int64_t* value_block_ptrs, int kv_head_stride, float scale,
+                        const int32_t* block_tables, int max_blocks_per_seq,
+                        const int32_t* context_lens, int max_context_len,
+                        const float* alibi_slopes, void* workspace, size_t workspace_bytes,
+                        void* stream);
+int dw4_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
+                                       int head_size, int block_size, int max_context_len,
+                                       size_t* workspace_bytes);
 
 #ifdef __cplusplus
 }

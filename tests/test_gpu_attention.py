@@ -1,0 +1,197 @@
+"""GPU parity of the paged KV cache ops and decode attention against
+oracle/attention.py, through the C ABI (LayerBlocksHolder, PagedAttention).
+
+Bars: cache writes and restores bit-exact (pure data movement); attention
+output within max|o - o_ref| <= 1e-2 * ||o_ref row||_inf of the float64
+oracle (softmax and both products in fp32 on the GPU, one fp16 rounding).
+Covers block sizes 16/32, head sizes 64/128/256, grouped-query heads (up to
+8 per kv head), ALiBi, ragged contexts (1 token, block edges, partitioned
+long contexts), padding slots, scattered and separately allocated blocks,
+determinism and the error statuses.  Every case prints its name before
+touching the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from hip_extends import _lib
+from operators import flags
+from operators.core.attention.common import AttentionConfig
+from operators.core.attention.real_page import PagedAttention
+from operators.core.block.common import BlockInfo
+from operators.core.block.real import LayerBlocksHolder
+from oracle import attention as A
+from oracle import gptq
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def say(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture
+def block_size(request):
+    old = flags.BLOCK_SIZE
+    flags.BLOCK_SIZE = request.param
+    yield request.param
+    flags.BLOCK_SIZE = old
+
+
+def _fill(holder, ctxs, kvh, hs, bs, seed, dev):
+    """Write each sequence's k, v through reshape_and_cache into scattered
+    blocks; returns tables, the token-major k, v and the numpy caches."""
+    rng = np.random.default_rng(seed)
+    nblocks = holder.layer_key_ptr_table_cpu.numel()
+    per = [(c + bs - 1) // bs for c in ctxs]
+    perm = rng.permutation(nblocks)
+    tables = np.zeros((len(ctxs), max(per)), np.int32)
+    kc, vc = A.empty_cache(nblocks, kvh, hs, bs, fill=0.0)
+    nxt = 0
+    for s, c in enumerate(ctxs):
+        tables[s, :per[s]] = perm[nxt:nxt + per[s]]
+        nxt += per[s]
+        k = rng.standard_normal((c, kvh, hs)).astype(np.float16)
+        v = rng.standard_normal((c, kvh, hs)).astype(np.float16)
+        slots = np.array([tables[s, t // bs] * bs + t % bs for t in range(c)], np.int64)
+        holder.kv_tensor_to_slots_with_convert(torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev),
+                                               torch.from_numpy(slots).to(dev))
+        A.reshape_and_cache(k, v, kc, vc, slots)
+    return tables, kc, vc
+
+
+@pytest.mark.parametrize("block_size", [16, 32], indirect=True)
+def test_cache_ops_bit_exact(hip_device, block_size):
+    bs = block_size
+    info = BlockInfo(head_dim=128, num_key_value_heads=4)
+    holder = LayerBlocksHolder.create_contigious_cacher(info, 12, hip_device)
+    kt, vt = holder.contigious_kv_tenosr
+    kt.zero_()
+    vt.zero_()
+    rng = np.random.default_rng(bs)
+    key = rng.standard_normal((30, 4, 128)).astype(np.float16)
+    val = rng.standard_normal((30, 4, 128)).astype(np.float16)
+    slots = rng.permutation(12 * bs)[:30].astype(np.int64)
+    slots[[2, 11]] = -1
+    say(f"reshape_and_cache bs={bs}")
+    holder.kv_tensor_to_slots_with_convert(torch.from_numpy(key).to(hip_device),
+                                           torch.from_numpy(val).to(hip_device),
+                                           torch.from_numpy(slots).to(hip_device))
+    torch.cuda.synchronize()
+    kc, vc = A.empty_cache(12, 4, 128, bs, fill=0.0)
+    A.reshape_and_cache(key, val, kc, vc, slots)
+    assert np.array_equal(kt.cpu().numpy().view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(vt.cpu().numpy().view(np.uint16), vc.view(np.uint16))
+    say(f"restore_from_cache bs={bs}")
+    k2, v2 = holder.kv_tensor_from_slots_with_convert_with_create(torch.from_numpy(slots).to(hip_device))
+    torch.cuda.synchronize()
+    keep = slots >= 0
+    assert np.array_equal(k2.cpu().numpy()[keep].view(np.uint16), key[keep].view(np.uint16))
+    assert np.array_equal(v2.cpu().numpy()[keep].view(np.uint16), val[keep].view(np.uint16))
+
+
+CASES = [
+    # seqs' context lengths, heads, kv heads, head size, block size, alibi
+    ([1, 7, 32, 20], 8, 8, 128, 32, False),      # one block: single partition
+    ([1, 16, 17, 100], 8, 8, 128, 16, False),
+    ([5, 64, 200], 8, 2, 64, 32, False),         # 4 query heads per kv head
+    ([512] * 8, 32, 32, 128, 16, False),         # the 7B stage's shape
+    ([300, 41], 32, 4, 128, 16, True),           # 8 per kv head, ALiBi
+    ([1500, 2049, 3], 4, 4, 128, 32, False),     # partitions of 512 tokens
+    ([33, 90], 6, 3, 256, 16, False),
+]
+
+
+@pytest.mark.parametrize("ctxs,heads,kvh,hs,bs,alibi", CASES)
+def test_paged_attention(hip_device, ctxs, heads, kvh, hs, bs, alibi):
+    old = flags.BLOCK_SIZE
+    flags.BLOCK_SIZE = bs
+    try:
+        info = BlockInfo(head_dim=hs, num_key_value_heads=kvh)
+        nblocks = sum((c + bs - 1) // bs for c in ctxs) + 5
+        holder = LayerBlocksHolder.create_contigious_cacher(info, nblocks, hip_device)
+        say(f"paged attention ctxs={ctxs} heads={heads}/{kvh} hs={hs} bs={bs} alibi={alibi}")
+        tables, kc, vc = _fill(holder, ctxs, kvh, hs, bs, len(ctxs) * heads + hs, hip_device)
+        rng = np.random.default_rng(99)
+        q = rng.standard_normal((len(ctxs), heads, hs)).astype(np.float16)
+        slopes = (2.0 ** -np.arange(1, heads + 1) * 8 / heads).astype(np.float32) if alibi else None
+        att = PagedAttention(AttentionConfig(heads * hs, hs, heads, kvh, heads // kvh))
+        lens = torch.tensor(ctxs, dtype=torch.int32, device=hip_device)
+        out = att.forward(torch.from_numpy(q).to(hip_device), max(ctxs), lens,
+                          torch.from_numpy(tables).to(hip_device), holder,
+                          None if slopes is None else torch.from_numpy(slopes).to(hip_device))
+        again = att.forward(torch.from_numpy(q).to(hip_device), max(ctxs), lens,
+                            torch.from_numpy(tables).to(hip_device), holder,
+                            None if slopes is None else torch.from_numpy(slopes).to(hip_device))
+        torch.cuda.synchronize()
+        assert torch.equal(out, again)  # deterministic
+        ref = A.paged_attention(q, kc, vc, tables, np.array(ctxs), att.scale, slopes)
+        y = out.float().cpu().numpy()
+        assert np.all(np.isfinite(y))
+        ok, worst = gptq.within_tolerance(y.reshape(-1, hs), ref.reshape(-1, hs), TOL)
+        assert ok, f"worst error ratio {worst:.3f}"
+    finally:
+        flags.BLOCK_SIZE = old
+
+
+def test_separately_allocated_blocks(hip_device):
+    """A pointer table over blocks allocated one by one (no contiguous backing),
+    the reference's swap-in case."""
+    bs, kvh, hs = flags.BLOCK_SIZE, 4, 128
+    info = BlockInfo(head_dim=hs, num_key_value_heads=kvh)
+    ks = [torch.zeros(info.key_block_shape, dtype=torch.float16, device=hip_device) for _ in range(9)]
+    vs = [torch.zeros(info.value_block_shape, dtype=torch.float16, device=hip_device) for _ in range(9)]
+    kp = [t.data_ptr() for t in ks]
+    vp = [t.data_ptr() for t in vs]
+    kc_t, vc_t = torch.tensor(kp), torch.tensor(vp)
+    holder = LayerBlocksHolder(info, kc_t.to(hip_device), vc_t.to(hip_device), kc_t, vc_t, kp, vp)
+    assert not holder.is_contigious
+    ctxs = [100, 65]
+    say("paged attention over separately allocated blocks")
+    tables, kc, vc = _fill(holder, ctxs, kvh, hs, bs, 5, hip_device)
+    q = np.random.default_rng(6).standard_normal((2, 8, hs)).astype(np.float16)
+    att = PagedAttention(AttentionConfig(8 * hs, hs, 8, kvh, 2))
+    out = att.forward(torch.from_numpy(q).to(hip_device), max(ctxs),
+                      torch.tensor(ctxs, dtype=torch.int32, device=hip_device),
+                      torch.from_numpy(tables).to(hip_device), holder)
+    torch.cuda.synchronize()
+    ref = A.paged_attention(q, kc, vc, tables, np.array(ctxs), att.scale)
+    ok, worst = gptq.within_tolerance(out.float().cpu().numpy().reshape(-1, hs), ref.reshape(-1, hs), TOL)
+    assert ok, worst
+
+
+def test_attention_statuses(hip_device):
+    lib = _lib.load()
+    sz = ctypes.c_size_t(0)
+    say("paged attention statuses")
+    assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 96, 16, 100, ctypes.byref(sz)) == \
+        _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_paged_attention_workspace_size(2, 36, 4, 128, 16, 100, ctypes.byref(sz)) == \
+        _lib.DW4_ERR_UNSUPPORTED  # 9 query heads per kv head
+    assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 128, 8, 100, ctypes.byref(sz)) == \
+        _lib.DW4_ERR_UNSUPPORTED  # block size 8
+    q = torch.zeros(4, 8, 128, dtype=torch.float16, device=hip_device)
+    o = torch.empty_like(q)
+    ptrs = torch.zeros(4, dtype=torch.int64, device=hip_device)
+    tab = torch.zeros(4, 64, dtype=torch.int32, device=hip_device)
+    lens = torch.ones(4, dtype=torch.int32, device=hip_device)
+    need = _lib.paged_attention_workspace_size(4, 8, 8, 128, 16, 1000)
+    assert need > 0
+    assert lib.dw4_paged_attention(4, 8, 8, 128, 16, q.data_ptr(), 1024, o.data_ptr(), 1024,
+                                   ptrs.data_ptr(), ptrs.data_ptr(), 2048, 0.1, tab.data_ptr(),
+                                   64, lens.data_ptr(), 1000, None, None, 0, None) == \
+        _lib.DW4_ERR_WORKSPACE
+    assert lib.dw4_paged_attention(4, 8, 8, 128, 16, q.data_ptr(), 1024, o.data_ptr(), 1024,
+                                   ptrs.data_ptr(), ptrs.data_ptr(), 2048, 0.1, tab.data_ptr(),
+                                   8, lens.data_ptr(), 1000, None, None, 0, None) == \
+        _lib.DW4_ERR_INVALID_ARG  # block table shorter than the context
+    assert lib.dw4_reshape_and_cache(3, 4, 100, 16, q.data_ptr(), 400, q.data_ptr(), 400,
+                                     ptrs.data_ptr(), ptrs.data_ptr(), 1600, ptrs.data_ptr(),
+                                     None) == _lib.DW4_ERR_UNSUPPORTED  # head size % 8
