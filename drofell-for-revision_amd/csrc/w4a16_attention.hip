@@ -113,15 +113,46 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
 
   const int32_t* btab = block_tables + (size_t)seq * max_blocks + t0 / BS;
   const int nb = (nt + BS - 1) / BS;
+  const int nbw = wave < nb ? (nb - wave + kAttnWaves - 1) / kAttnWaves : 0;  // this wave's blocks
   const int tt = lane % BS;   // token of this lane within a block
   const int sg = lane / BS;   // slice group
-  // q . k
-  for (int b = wave; b < nb; b += kAttnWaves) {
-    const uint16_t* kb = reinterpret_cast<const uint16_t*>(kptr[btab[b]]) +
-                         (size_t)kvh * kv_head_stride;
-    h8 kv[SPL];
+  // Each wave keeps its next NPF blocks' keys and values in flight: the
+  // value loads of the first blocks are issued with the key loads, before
+  // the softmax, so their latency overlaps q . k.
+  constexpr int NPF = 2;
+  h8 kreg[NPF][SPL];
+  h8 vreg[NPF][DPL][BS / 8];
+  auto kbase = [&](int i) {
+    return reinterpret_cast<const uint16_t*>(kptr[btab[wave + kAttnWaves * i]]) +
+           (size_t)kvh * kv_head_stride;
+  };
+  auto vbase = [&](int i) {
+    return reinterpret_cast<const uint16_t*>(vptr[btab[wave + kAttnWaves * i]]) +
+           (size_t)kvh * kv_head_stride;
+  };
+  auto load_k = [&](int slot, int i) {
+    const uint16_t* kb = kbase(i);
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) kv[j] = *(const h8*)(kb + ((sg + TPL * j) * BS + tt) * 8);
+    for (int j = 0; j < SPL; ++j) kreg[slot][j] = *(const h8*)(kb + ((sg + TPL * j) * BS + tt) * 8);
+  };
+  auto load_v = [&](int slot, int i) {
+    const uint16_t* vb = vbase(i);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+#pragma unroll
+      for (int u = 0; u < BS / 8; ++u)
+        vreg[slot][j][u] = *(const h8*)(vb + (size_t)(lane + 64 * j) * BS + 8 * u);
+  };
+#pragma unroll
+  for (int u = 0; u < NPF; ++u)
+    if (u < nbw) {
+      load_k(u, u);
+      load_v(u, u);
+    }
+
+  // q . k
+  auto qk = [&](int slot, int i) {
+    const int b = wave + kAttnWaves * i;
     float dot[GMAX];
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
@@ -131,7 +162,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
         for (int j = 0; j < SPL; ++j) {
           const float* qv = qs + g * HS + (sg + TPL * j) * 8;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dot[g] = fmaf(qv[e], (float)kv[j][e], dot[g]);
+          for (int e = 0; e < 8; ++e) dot[g] = fmaf(qv[e], (float)kreg[slot][j][e], dot[g]);
         }
       }
     }
@@ -149,6 +180,16 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
           if (alibi != nullptr) l += alibi[h0 + g] * (float)(t - ctx + 1);
           logit[g * part_tokens + b * BS + tt] = t < t1 ? l : -FLT_MAX;
         }
+      }
+    }
+  };
+  for (int i0 = 0; i0 < nbw; i0 += NPF) {
+#pragma unroll
+    for (int u = 0; u < NPF; ++u) {
+      const int i = i0 + u;
+      if (i < nbw) {
+        qk(u, i);
+        if (i + NPF < nbw) load_k(u, i + NPF);
       }
     }
   }
@@ -181,25 +222,30 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   for (int g = 0; g < GMAX; ++g)
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
-  for (int b = wave; b < nb; b += kAttnWaves) {
-    const uint16_t* vb = reinterpret_cast<const uint16_t*>(vptr[btab[b]]) +
-                         (size_t)kvh * kv_head_stride;
+  auto pv = [&](int slot, int i) {
+    const int b = wave + kAttnWaves * i;
     const int valid = min(BS, nt - b * BS);  // tokens of this block in the context
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const uint16_t* row = vb + (size_t)(lane + 64 * j) * BS;
+    for (int j = 0; j < DPL; ++j)
 #pragma unroll
-      for (int u = 0; u < BS / 8; ++u) {
-        const h8 v = *(const h8*)(row + 8 * u);
+      for (int u = 0; u < BS / 8; ++u)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int tb = 8 * u + e;
           // slots past the context may hold anything: never multiply them
-          const float vf = tb < valid ? (float)v[e] : 0.f;
+          const float vf = tb < valid ? (float)vreg[slot][j][u][e] : 0.f;
 #pragma unroll
           for (int g = 0; g < GMAX; ++g)
             if (g < G) acc[g][j] = fmaf(logit[g * part_tokens + b * BS + tb], vf, acc[g][j]);
         }
+  };
+  for (int i0 = 0; i0 < nbw; i0 += NPF) {
+#pragma unroll
+    for (int u = 0; u < NPF; ++u) {
+      const int i = i0 + u;
+      if (i < nbw) {
+        pv(u, i);
+        if (i + NPF < nbw) load_v(u, i + NPF);
       }
     }
   }
@@ -244,13 +290,27 @@ paged_attention_reduce_kernel(uint16_t* __restrict__ out, int64_t o_stride, int 
   const int ctx = min(context_lens[seq], max_tokens);
   const int parts = min(num_parts, (ctx + part_tokens - 1) / part_tokens);
   const size_t r0 = ((size_t)seq * num_heads + h) * num_parts;
-  float gmax = -FLT_MAX;
-  for (int p = 0; p < parts; ++p) gmax = fmaxf(gmax, ws_ml[2 * (r0 + p)]);
-  float total = 0.f, o = 0.f;
-  for (int p = 0; p < parts; ++p) {
-    const float w = __expf(ws_ml[2 * (r0 + p)] - gmax);
-    total += ws_ml[2 * (r0 + p) + 1] * w;
-    o += ws_out[(r0 + p) * HS + d] * w;
+  // Running max and rescaled sums over the partitions in order; the loads
+  // of a batch of 8 partitions are all in flight before the first update.
+  float gmax = -FLT_MAX, total = 0.f, o = 0.f;
+  for (int p0 = 0; p0 < parts; p0 += 8) {
+    float m[8], l[8], v[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool in = p0 + b < parts;
+      m[b] = in ? ws_ml[2 * (r0 + p0 + b)] : -FLT_MAX;
+      l[b] = in ? ws_ml[2 * (r0 + p0 + b) + 1] : 0.f;
+      v[b] = in ? ws_out[(r0 + p0 + b) * HS + d] : 0.f;
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (p0 + b >= parts) break;
+      const float nm = fmaxf(gmax, m[b]);
+      const float a = __expf(gmax - nm), w = __expf(m[b] - nm);
+      total = total * a + l[b] * w;
+      o = o * a + v[b] * w;
+      gmax = nm;
+    }
   }
   out[(size_t)seq * o_stride + (size_t)h * HS + d] = h_bits((_Float16)(o / total));
 }
@@ -328,7 +388,8 @@ PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_siz
                                    int max_context_len, int cus) {
   PagedAttnPlan p;
   const int blocks = std::max(1, (max_context_len + block_size - 1) / block_size);
-  // about four workgroups per CU; partitions of whole blocks, at most 512 tokens
+  // about four workgroups per CU (eight measured no faster); partitions of
+  // whole blocks, at most 512 tokens
   const int pairs = std::max(1, num_seqs * num_kv_heads);
   int parts = std::max(1, (4 * cus + pairs - 1) / pairs);
   parts = std::min(parts, blocks);
