@@ -119,7 +119,8 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   // Each wave keeps its next NPF blocks' keys and values in flight: the
   // value loads of the first blocks are issued with the key loads, before
   // the softmax, so their latency overlaps q . k.
-  constexpr int NPF = 2;
+  // (one block for the widest variants, whose unrolled p . v would not fit)
+  constexpr int NPF = DPL * (BS / 8) * GMAX <= 16 ? 2 : 1;
   h8 kreg[NPF][SPL];
   h8 vreg[NPF][DPL][BS / 8];
   auto kbase = [&](int i) {
@@ -304,12 +305,13 @@ paged_attention_reduce_kernel(uint16_t* __restrict__ out, int64_t o_stride, int 
     }
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      if (p0 + b >= parts) break;
-      const float nm = fmaxf(gmax, m[b]);
-      const float a = __expf(gmax - nm), w = __expf(m[b] - nm);
-      total = total * a + l[b] * w;
-      o = o * a + v[b] * w;
-      gmax = nm;
+      if (p0 + b < parts) {
+        const float nm = fmaxf(gmax, m[b]);
+        const float a = __expf(gmax - nm), w = __expf(m[b] - nm);
+        total = total * a + l[b] * w;
+        o = o * a + v[b] * w;
+        gmax = nm;
+      }
     }
   }
   out[(size_t)seq * o_stride + (size_t)h * HS + d] = h_bits((_Float16)(o / total));
