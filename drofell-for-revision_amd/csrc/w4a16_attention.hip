@@ -384,7 +384,45 @@ hipError_t launch_pa_bs(const PagedAttnArgs& a, const PagedAttnPlan& p, float* w
   return launch_pa_g<HS, 32>(a, p, ws, stream);
 }
 
+// Rotary embedding, rotate-half form, in place on fp16 rows [batch][rows][hd]
+// (row = token * heads + head): position p = past + row / heads, pair
+// (l, r) = (x[c], x[c + hd/2]):
+//   l' = fma(l, cos[p][c], fp16(r * -sin[p][c]))
+//   r' = fma(r, cos[p][c + hd/2], fp16(l * sin[p][c + hd/2]))
+// each product and each fma rounded once in fp16, as the reference's
+// half-precision kernel (cuda_extends/exllama/fuse_v2/rope.cu:24-91) does.
+__global__ void rope_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ sinp,
+                            const uint16_t* __restrict__ cosp, int rows, int hd, int heads,
+                            int max_pos, int past_len, const int32_t* __restrict__ past_lens) {
+  const int half = hd / 2;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = (int)(i % half);
+  const int64_t row = i / half;  // within this batch entry
+  if (row >= rows) return;
+  const int b = blockIdx.y;
+  const int pos = (past_len >= 0 ? past_len : past_lens[b]) + (int)(row / heads);
+  if (pos < 0 || pos >= max_pos) return;  // outside the table: row left as it is
+  uint16_t* xr = x + ((int64_t)b * rows + row) * hd;
+  const _Float16 l = as_h(xr[c]), r = as_h(xr[c + half]);
+  const _Float16 cl = as_h(cosp[(int64_t)pos * hd + c]), cr = as_h(cosp[(int64_t)pos * hd + c + half]);
+  const _Float16 sl = as_h(sinp[(int64_t)pos * hd + c]), sr = as_h(sinp[(int64_t)pos * hd + c + half]);
+  const _Float16 ls = r * (_Float16)(-sl);
+  const _Float16 rs = l * sr;
+  xr[c] = h_bits(__builtin_fmaf16(l, cl, ls));
+  xr[c + half] = h_bits(__builtin_fmaf16(r, cr, rs));
+}
+
 }  // namespace
+
+hipError_t launch_rope(uint16_t* x, const uint16_t* sinp, const uint16_t* cosp, int batch,
+                       int rows, int hd, int heads, int max_pos, int past_len,
+                       const int32_t* past_lens, hipStream_t stream) {
+  const int64_t n = (int64_t)rows * (hd / 2);
+  const dim3 grid((unsigned)((n + 255) / 256), (unsigned)batch);
+  rope_kernel<<<grid, 256, 0, stream>>>(x, sinp, cosp, rows, hd, heads, max_pos, past_len,
+                                        past_lens);
+  return hipGetLastError();
+}
 
 PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_size,
                                    int max_context_len, int cus) {

@@ -408,6 +408,19 @@ int dw4_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_
                                                static_cast<hipStream_t>(stream)));
 }
 
+int dw4_rope(int batch_size, int rows_per_batch, int num_heads, int head_dim, uint16_t* x,
+             const uint16_t* sin_table, const uint16_t* cos_table, int max_positions, int past_len,
+             const int32_t* past_lens, void* stream) {
+  if (batch_size < 0 || rows_per_batch < 0 || num_heads <= 0 || head_dim <= 0 || max_positions < 0)
+    return DW4_ERR_INVALID_ARG;
+  if (head_dim % 2 != 0 || rows_per_batch % num_heads != 0) return DW4_ERR_INVALID_ARG;
+  if (batch_size == 0 || rows_per_batch == 0) return DW4_OK;
+  if (!x || !sin_table || !cos_table || (past_len < 0 && !past_lens)) return DW4_ERR_INVALID_ARG;
+  return status_of(dw4::launch_rope(x, sin_table, cos_table, batch_size, rows_per_batch, head_dim,
+                                    num_heads, max_positions, past_len, past_lens,
+                                    static_cast<hipStream_t>(stream)));
+}
+
 int dw4_gemm_t_workspace_size(int m, int k, int n, int group_size, size_t* workspace_bytes) {
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;

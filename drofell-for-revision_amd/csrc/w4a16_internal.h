@@ -238,4 +238,9 @@ hipError_t launch_reshape_and_cache(uint16_t* key, int64_t key_stride, uint16_t*
                                     int head_size, int block_size, int kv_head_stride,
                                     bool restore, hipStream_t stream);
 
+// Rotary embedding in place on fp16 rows [batch][rows][hd] (reference half-precision form).
+hipError_t launch_rope(uint16_t* x, const uint16_t* sinp, const uint16_t* cosp, int batch,
+                       int rows, int hd, int heads, int max_pos, int past_len,
+                       const int32_t* past_lens, hipStream_t stream);
+
 }  // namespace dw4

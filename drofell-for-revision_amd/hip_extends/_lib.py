@@ -72,6 +72,8 @@ SIGNATURES = {
     "dw4_paged_attention_workspace_size": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                                       _c.c_int, _c.c_int,
                                                       _c.POINTER(_c.c_size_t)]),
+    "dw4_rope": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _c.c_int,
+                            _c.c_int, _P, _P]),
     "dw4_gemm_group": (_c.c_int, [_c.c_int, _IP, _c.c_int, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_silu_mul": (_c.c_int, [_c.c_int, _P, _c.c_int64, _IP, _IP, _P, _c.c_int64,
                                      _P, _c.c_size_t, _P]),
@@ -85,7 +87,7 @@ SIGNATURES = {
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -568,6 +568,30 @@ def attention_forward_qkv_stage_v2_py(layernorm: torch.Tensor, norm_epsilon: flo
         ctypes.byref(items[2]), ws.data_ptr(), ws.numel(), _stream(x.device)))
 
 
+def attention_forward_rope_stage_v2_py(temp_q_output: torch.Tensor, temp_k_output: torch.Tensor,
+                                       sin: torch.Tensor, cos: torch.Tensor, q_len: int,
+                                       batch_size: int, num_heads: int, num_kv_heads: int,
+                                       head_dim: int, past_len: int,
+                                       past_lens: Optional[torch.Tensor]) -> None:
+    """Rotary embedding of q and k in place (``exllama.py:133-135`` ->
+    ``fuse_v2/rope.cu``): row r of batch entry b takes position
+    ``(past_len if past_len >= 0 else past_lens[b]) + r // heads`` of the fp16
+    tables ``sin`` / ``cos`` [max_positions, head_dim]."""
+    lens = None
+    if past_len < 0:
+        if past_lens is None:
+            raise ValueError("past_len -1 needs past_lens")
+        lens = past_lens.to(device=temp_q_output.device, dtype=torch.int32).contiguous()
+    s16 = sin.to(torch.float16).contiguous()
+    c16 = cos.to(torch.float16).contiguous()
+    for t, heads in ((temp_q_output, num_heads), (temp_k_output, num_kv_heads)):
+        if t.dtype != torch.float16 or not t.is_contiguous():
+            raise TypeError("q/k must be contiguous fp16")
+        _lib.call("dw4_rope", batch_size, q_len * heads, heads, head_dim, t.data_ptr(),
+                  s16.data_ptr(), c16.data_ptr(), s16.shape[0], past_len,
+                  None if lens is None else lens.data_ptr(), _stream(t.device))
+
+
 def mlp_forward_v2_py(layernorm: torch.Tensor, norm_epsilon: float, gate_q4: Any, up_q4: Any,
                       down_q4: Any, temp_rms_output: torch.Tensor,
                       temp_gate_output: torch.Tensor, temp_up_output: torch.Tensor,

@@ -23,6 +23,8 @@
  *                    (cuda_extends/vllm/attention/attention_kernels.cu:1602-1843)
  *                    as operators/core/attention/real_page.py:23-189 and
  *                    operators/core/block/real.py:66-106 call them
+ *   dw4_rope         rope_cuda (cuda_extends/exllama/fuse_v2/rope.cu:24-135), the
+ *                    RoPE half of attention_forward_rope_stage_v2
  *   dw4_gemm_t       q4_transpose_matmul_blas_v2 (entry.cpp:392-429 ->
  *                    exllama/q4_transpose_matmul.cu:115-167), the PEFT backward
  *                    of Q4MatrixV2.transpose_matmul (exllama.py:528-544)
@@ -95,7 +97,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 5
+#define DW4_ABI_VERSION 6
 
 enum {
   DW4_OK = 0,
@@ -320,6 +322,19 @@ int dw4_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_
 int dw4_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
                                        int head_size, int block_size, int max_context_len,
                                        size_t* workspace_bytes);
+
+/* Rotary embedding (rotate-half form) in place on fp16 x
+ * [batch_size][rows_per_batch][head_dim], rows_per_batch = tokens *
+ * num_heads: row r of batch entry b takes position
+ * (past_len >= 0 ? past_len : past_lens[b]) + r / num_heads of the fp16
+ * tables sin_table, cos_table [max_positions][head_dim]; rows whose
+ * position is outside the tables are left as they are.  Each product and
+ * fused multiply-add is rounded once in fp16, as the reference's
+ * half-precision kernel does.  Replaces rope_cuda / the RoPE half of
+ * attention_forward_rope_stage_v2 (cuda_extends/exllama/fuse_v2/rope.cu:24-135). */
+int dw4_rope(int batch_size, int rows_per_batch, int num_heads, int head_dim, uint16_t* x,
+             const uint16_t* sin_table, const uint16_t* cos_table, int max_positions, int past_len,
+             const int32_t* past_lens, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,9 @@ Restates in numpy (paths relative to ``/root/reference/After-Revision-DROFELL``)
   ``[head][d][slot % bs]`` (x = 8 for fp16, ``operators/core/block/common.py:7-60``);
   negative slots are padding and skipped;
 * ``restore_from_cache`` -- ``cache_kernels.cu:332-375``, the reverse copy;
+* ``rope`` -- ``cuda_extends/exllama/fuse_v2/rope.cu:24-91`` (rotate-half
+  rotary embedding in fp16 arithmetic, each product and fma rounded once;
+  ``fp16_round`` is an exact round-to-nearest-even of a rational value);
 * ``paged_attention`` -- ``cuda_extends/vllm/attention/attention_kernels.cu``
   (v1 / v2 compute the same function): for sequence s and query head h
   (kv head ``h // (heads // kv_heads)``, ``operators/core/attention/real_page.py:19-22``),
@@ -101,3 +104,75 @@ def paged_attention(query: np.ndarray, key_cache: np.ndarray, value_cache: np.nd
             p = np.exp(logits - logits.max())
             out[s, h] = (p / p.sum()) @ v[:, g, :]
     return out
+
+
+def fp16_round(v) -> np.float16:
+    """Exact value ``v`` (a Fraction or int) rounded once to IEEE binary16,
+    to nearest, ties to even (subnormals down to 2**-24, overflow to inf)."""
+    from fractions import Fraction
+    v = Fraction(v)
+    if v == 0:
+        return np.float16(0.0)
+    sign = -1 if v < 0 else 1
+    a = -v if v < 0 else v
+    if a >= 65520:  # halfway between 65504 and 2**16 and above
+        return np.float16(sign * np.inf)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1  # now 2**e <= a < 2**(e + 1)
+    q = Fraction(2) ** (max(e, -14) - 10)  # spacing of binary16 values near a
+    n = a / q
+    m = n.numerator // n.denominator
+    rem = n - m
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and m % 2 == 1):
+        m += 1
+    return np.float16(sign * float(m * q))
+
+
+def _fp16_fma(a: np.float16, b: np.float16, c: np.float16) -> np.float16:
+    """a * b + c with one rounding (IEEE fusedMultiplyAdd in binary16)."""
+    from fractions import Fraction
+    p = Fraction(float(a)) * Fraction(float(b))
+    exact = p + Fraction(float(c))
+    if exact == 0:
+        # an exact zero is +0 under round-to-nearest, unless the product and
+        # the addend are both zeros of negative sign
+        neg_product = p == 0 and bool(np.signbit(a) != np.signbit(b))
+        neg_addend = float(c) == 0 and bool(np.signbit(c))
+        return np.float16(-0.0) if (neg_product and neg_addend) else np.float16(0.0)
+    return fp16_round(exact)
+
+
+def rope(x: np.ndarray, sin: np.ndarray, cos: np.ndarray, num_heads: int, past_len: int,
+         past_lens: Optional[np.ndarray] = None) -> np.ndarray:
+    """``cuda_extends/exllama/fuse_v2/rope.cu:24-91`` on fp16 x
+    [batch, rows, hd] (row = token * heads + head): position
+    ``past + row // heads``; pair (l, r) = (x[c], x[c + hd/2]):
+    ``l' = fma(l, cos[c], fp16(r * -sin[c]))``,
+    ``r' = fma(r, cos[c + hd/2], fp16(l * sin[c + hd/2]))``, every product
+    and fma rounded once to fp16.  Rows whose position falls outside the
+    tables are returned unchanged."""
+    out = x.copy()
+    batch, rows, hd = x.shape
+    half = hd // 2
+    for b in range(batch):
+        base = past_len if past_len >= 0 else int(past_lens[b])
+        for r in range(rows):
+            pos = base + r // num_heads
+            if pos < 0 or pos >= sin.shape[0]:
+                continue
+            for c in range(half):
+                lv, rv = x[b, r, c], x[b, r, c + half]
+                ls = np.float16(np.float32(rv) * -np.float32(sin[pos, c]))  # exact product, one rounding
+                rs = np.float16(np.float32(lv) * np.float32(sin[pos, c + half]))
+                out[b, r, c] = _fp16_fma(lv, cos[pos, c], ls)
+                out[b, r, c + half] = _fp16_fma(rv, cos[pos, c + half], rs)
+    return out
+
+
+def rope_tables(max_pos: int, hd: int, theta: float = 10000.0):
+    """Llama's fp16 sin/cos tables [max_pos, hd] (the rotate-half layout)."""
+    inv = 1.0 / theta ** (np.arange(0, hd, 2, dtype=np.float64) / hd)
+    ang = np.outer(np.arange(max_pos, dtype=np.float64), inv)
+    ang = np.concatenate([ang, ang], axis=1)
+    return np.sin(ang).astype(np.float16), np.cos(ang).astype(np.float16)

@@ -195,3 +195,24 @@ def test_attention_statuses(hip_device):
     assert lib.dw4_reshape_and_cache(3, 4, 100, 16, q.data_ptr(), 400, q.data_ptr(), 400,
                                      ptrs.data_ptr(), ptrs.data_ptr(), 1600, ptrs.data_ptr(),
                                      None) == _lib.DW4_ERR_UNSUPPORTED  # head size % 8
+
+
+@pytest.mark.parametrize("past", [3, -1])
+def test_rope_bit_exact(hip_device, past):
+    from hip_extends.w4a16 import attention_forward_rope_stage_v2_py
+    rng = np.random.default_rng(21)
+    batch, q_len, heads, kvh, hd = 3, 2, 4, 2, 128
+    sin, cos = A.rope_tables(40, hd)
+    q = (rng.standard_normal((batch, q_len * heads, hd)) * 3).astype(np.float16)
+    k = (rng.standard_normal((batch, q_len * kvh, hd)) * 3).astype(np.float16)
+    lens = np.array([0, 17, 39], np.int32)  # the last one runs past the table (row left as is)
+    say(f"rope past={past}")
+    qd, kd = torch.from_numpy(q).to(hip_device), torch.from_numpy(k).to(hip_device)
+    attention_forward_rope_stage_v2_py(qd, kd, torch.from_numpy(sin).to(hip_device),
+                                       torch.from_numpy(cos).to(hip_device), q_len, batch, heads,
+                                       kvh, hd, past, torch.from_numpy(lens).to(hip_device))
+    torch.cuda.synchronize()
+    qr = A.rope(q, sin, cos, heads, past, lens)
+    kr = A.rope(k, sin, cos, kvh, past, lens)
+    assert np.array_equal(qd.cpu().numpy().view(np.uint16), qr.view(np.uint16))
+    assert np.array_equal(kd.cpu().numpy().view(np.uint16), kr.view(np.uint16))

@@ -160,3 +160,50 @@ def test_checks_catch_planted_mistakes():
     for kind in ("offset", "head_map", "no_scale", "value_layout"):
         assert not np.allclose(mutant(kind), ref, rtol=1e-3, atol=1e-3), kind
     assert np.allclose(A.paged_attention(q, kc, vc, tables, lens, scale), ref)
+
+
+def test_fp16_round_matches_numpy():
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 5, 3000),
+                           [65504.0, 65519.99, 65520.0, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8, 0.0]])
+    for v in vals:
+        got = A.fp16_round(Fraction(float(v)))
+        want = np.float16(np.float64(v))  # numpy's conversion rounds once, to nearest even
+        assert got.view(np.uint16) == want.view(np.uint16) or (np.isnan(got) and np.isnan(want)), v
+    # exact ties go to the even neighbour
+    assert A.fp16_round(Fraction(2049, 2)) == np.float16(1024.0)
+    assert A.fp16_round(Fraction(2051, 2)) == np.float16(1026.0)
+
+
+def test_rope_closed_forms_and_mistakes():
+    rng = np.random.default_rng(8)
+    hd, heads = 16, 2
+    sin, cos = A.rope_tables(8, hd)
+    x = rng.standard_normal((2, 3 * heads, hd)).astype(np.float16)
+    # position 0: sin = 0, cos = 1 -> identity
+    y0 = A.rope(x[:, :heads], sin, cos, heads, 0)
+    assert np.array_equal(y0, x[:, :heads])
+    # a rotation keeps each (l, r) pair's length (to fp16 rounding)
+    y = A.rope(x, sin, cos, heads, 2)
+    h = hd // 2
+    n0 = x[..., :h].astype(np.float64) ** 2 + x[..., h:].astype(np.float64) ** 2
+    n1 = y[..., :h].astype(np.float64) ** 2 + y[..., h:].astype(np.float64) ** 2
+    assert np.allclose(n0, n1, rtol=5e-3, atol=1e-3)
+    # matches the float64 rotation to fp16 accuracy
+    for b in range(2):
+        for r in range(3 * heads):
+            p = 2 + r // heads
+            c, s = cos[p].astype(np.float64), sin[p].astype(np.float64)
+            l, rr = x[b, r, :h].astype(np.float64), x[b, r, h:].astype(np.float64)
+            ref = np.concatenate([l * c[:h] - rr * s[:h], rr * c[h:] + l * s[h:]])
+            assert np.allclose(y[b, r], ref, rtol=2e-3, atol=2e-3)
+    # per-batch positions and rows outside the table
+    y2 = A.rope(x, sin, cos, heads, -1, np.array([2, 6]))
+    assert np.array_equal(y2[0], y[0])
+    assert np.array_equal(y2[1, 4:], x[1, 4:])  # positions 8 and up: unchanged
+    # planted mistakes: halves swapped, or the token index ignored
+    bad = y.copy()
+    bad[..., :h], bad[..., h:] = y[..., h:], y[..., :h]
+    assert not np.array_equal(bad, y)
+    assert not np.array_equal(A.rope(x, sin, cos, 3 * heads, 2), y)
