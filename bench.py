@@ -37,7 +37,8 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None):
+def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None,
+                   scale_mul: float = 0.01):
     import torch
     from gptq_synth import LLAMA2_7B_SHAPES
     from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
@@ -55,8 +56,8 @@ def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None)
                                     device=dev, generator=gen)
             qzeros = torch.randint(-2 ** 31, 2 ** 31, (groups, n // 8), dtype=torch.int32,
                                    device=dev, generator=gen)
-            scales = (torch.randn(groups, n, device=dev, generator=gen).abs() * 0.01
-                      + 1e-3).to(torch.float16)
+            scales = (torch.randn(groups, n, device=dev, generator=gen).abs() * scale_mul
+                      + scale_mul / 10).to(torch.float16)
             q4 = Q4MatrixV2(qweight, qzeros, scales, k, n, None, False, tp, cache)
             mats.append((name, k, n, q4))
             del qweight, qzeros, scales
@@ -104,6 +105,120 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / steps
     return ms, wall, sel
+
+
+def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_size: int,
+              warmup: int) -> dict:
+    """The 8-layer Llama-2-7B decoder stage at decode: per layer the fused
+    q/k/v stage (RMSNorm + grouped q/k/v), RoPE, the KV-cache write, paged
+    attention and the after-attention stage (o_proj + residual, RMSNorm,
+    gate/up with SiLU*mul, down + residual), for `batch` sequences whose
+    cached context grows from `ctx0` by one token per step.  One step (all
+    layers) is captured into a HIP graph; positions, slots and context
+    lengths advance on the device inside it."""
+    import torch
+    from gptq_synth import LLAMA2_7B_SHAPES
+    from hip_extends.w4a16 import (attention_forward_qkv_stage_v2_py,
+                                   attention_forward_rope_stage_v2_py, decoder_after_stage_v2_py)
+    from operators import flags
+    from operators.core.attention.common import AttentionConfig
+    from operators.core.attention.real_page import PagedAttention
+    from operators.core.block.common import BlockInfo
+    from operators.core.block.real import LayerBlocksHolder
+
+    hidden, inter, heads, hd = 4096, 11008, 32, 128
+    flags.BLOCK_SIZE = block_size
+    max_ctx = ctx0 + decode_steps
+    mats, cache = build_matrices(dev, layers, batch, seed0=777, scale_mul=0.002)
+    per = len(LLAMA2_7B_SHAPES)
+    lay = [{name: q4 for name, _, _, q4 in mats[i * per:(i + 1) * per]} for i in range(layers)]
+    info = BlockInfo(head_dim=hd, num_key_value_heads=heads)
+    bps = (max_ctx + block_size - 1) // block_size  # blocks per sequence
+    holders = []
+    for _ in range(layers):
+        h = LayerBlocksHolder.create_contigious_cacher(info, batch * bps, dev)
+        kc, vc = h.contigious_kv_tenosr
+        kc.normal_()
+        vc.normal_()
+        holders.append(h)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    tables = torch.randperm(batch * bps, device=dev, generator=gen).to(torch.int32).view(batch, bps)
+    tflat = tables.to(torch.int64).view(-1)
+    att = PagedAttention(AttentionConfig(hidden, hd, heads, heads, 1))
+    att.workspace(batch, max_ctx, dev)
+    inv = 1.0 / 10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float64) / hd)
+    ang = torch.outer(torch.arange(max_ctx + 1, dtype=torch.float64), inv)
+    ang = torch.cat([ang, ang], dim=1)
+    sin, cos = ang.sin().to(dev, torch.float16), ang.cos().to(dev, torch.float16)
+    f16 = dict(dtype=torch.float16, device=dev)
+    embed = (torch.randn(batch, hidden, device=dev, generator=gen)).to(torch.float16)
+    xa, xb = torch.empty(batch, hidden, **f16), torch.empty(batch, hidden, **f16)
+    rms, q, k, v = (torch.empty(batch, hidden, **f16) for _ in range(4))
+    x2 = torch.empty(batch, hidden, **f16)
+    hbuf, ubuf = torch.empty(batch, inter, **f16), torch.empty(batch, inter, **f16)
+    norm = torch.ones(hidden, **f16)
+    ctx = torch.full((batch,), ctx0, dtype=torch.int32, device=dev)
+    rows = torch.arange(batch, device=dev, dtype=torch.int64) * bps
+
+    def step():
+        xa.copy_(embed)  # each step's new tokens (synthetic embeddings)
+        pos = ctx.clone()
+        slots = tflat[rows + (pos // block_size).to(torch.int64)] * block_size + \
+            (pos % block_size).to(torch.int64)
+        lens = pos + 1
+        xin, xout = xa, xb
+        for li in range(layers):
+            w = lay[li]
+            attention_forward_qkv_stage_v2_py(norm, 1e-5, w["q_proj"], w["k_proj"], w["v_proj"],
+                                              rms, q, k, v, None, xin, 0, 0, 0, 1, batch)
+            attention_forward_rope_stage_v2_py(q, k, sin, cos, 1, batch, heads, heads, hd, -1, pos)
+            holders[li].kv_tensor_to_slots_with_convert(k.view(batch, heads, hd),
+                                                        v.view(batch, heads, hd), slots)
+            o = att.forward(q.view(batch, heads, hd), max_ctx, lens, tables, holders[li])
+            decoder_after_stage_v2_py(w["o_proj"], w["gate_proj"], w["up_proj"], w["down_proj"],
+                                      norm, 1e-5, o.view(batch, hidden), xin, x2, rms, hbuf, ubuf,
+                                      xout)
+            xin, xout = xout, xin
+        ctx.add_(1)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    ctx.fill_(ctx0)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(decode_steps):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    ms = start.elapsed_time(end) / decode_steps
+    finite = bool(torch.isfinite(xa).all().item() and torch.isfinite(xb).all().item())
+    kv_bytes = layers * batch * (ctx0 + decode_steps / 2) * heads * hd * 2 * 2
+    wbytes = sum(q4.qweight.numel() * 4 + q4.scales.numel() * 2 + q4.qzeros.numel() * 4
+                 for _, _, _, q4 in mats)
+    del graph, holders, mats, cache
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": round(batch / (ms * 1e-3), 1), "ms_per_step": round(ms, 4),
+            "batch": batch, "layers": layers, "context": [ctx0, max_ctx],
+            "decode_steps": decode_steps, "block_size": block_size,
+            "weight_bytes": wbytes, "mean_kv_bytes_per_step": int(kv_bytes),
+            "hbm_gbs": round((wbytes + kv_bytes) / (ms * 1e-3) / 1e9, 1), "finite": finite,
+            "workload": ("8 Llama-2-7B decoder layers (GPTQ g128 asymmetric), per layer: "
+                         "RMSNorm+q/k/v, RoPE, KV-cache write, paged attention (32 heads x 128, "
+                         "fp16 KV), o_proj+residual, RMSNorm, gate/up+SiLU*mul, down+residual")}
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -165,6 +280,12 @@ def main() -> int:
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the M=--prefill-m leg (for hardware-counter passes)")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
+    ap.add_argument("--no-stage", action="store_true",
+                    help="skip the decoder-stage leg (GEMMs + RoPE + KV cache + paged attention)")
+    ap.add_argument("--stage-batch", type=int, default=8)
+    ap.add_argument("--stage-context", type=int, default=512)
+    ap.add_argument("--stage-steps", type=int, default=128)
+    ap.add_argument("--stage-block-size", type=int, default=16)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -292,6 +413,15 @@ def main() -> int:
             sweep(mmats, dev, max(5, args.steps // 5), 3,
                   shapes=((4096, 12288), (4096, 22016)))
         del mmats, _mcache
+
+    if not args.no_stage:
+        mats.clear()
+        torch.cuda.empty_cache()
+        st = stage_leg(dev, args.layers, args.stage_batch, args.stage_context, args.stage_steps,
+                       args.stage_block_size, max(2, args.warmup // 2))
+        log(f"stage decode batch {st['batch']}: {st['ms_per_step'] * 1e3:.1f} us per step, "
+            f"{st['tokens_per_s']:.0f} tokens/s, {st['hbm_gbs']:.0f} GB/s (weights + KV)")
+        result["stage"] = st
 
     if not args.no_cpu:
         log("timing CPU baseline")
