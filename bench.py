@@ -118,8 +118,7 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
     lengths advance on the device inside it."""
     import torch
     from gptq_synth import LLAMA2_7B_SHAPES
-    from hip_extends.w4a16 import (attention_forward_qkv_stage_v2_py,
-                                   attention_forward_rope_stage_v2_py, decoder_after_stage_v2_py)
+    from hip_extends.w4a16 import attention_forward_qkv_stage_v2_py, decoder_after_stage_v2_py
     from operators import flags
     from operators.core.attention.common import AttentionConfig
     from operators.core.attention.real_page import PagedAttention
@@ -144,7 +143,6 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
     tables = torch.randperm(batch * bps, device=dev, generator=gen).to(torch.int32).view(batch, bps)
-    tflat = tables.to(torch.int64).view(-1)
     att = PagedAttention(AttentionConfig(hidden, hd, heads, heads, 1))
     att.workspace(batch, max_ctx, dev)
     inv = 1.0 / 10000.0 ** (torch.arange(0, hd, 2, dtype=torch.float64) / hd)
@@ -159,22 +157,20 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
     hbuf, ubuf = torch.empty(batch, inter, **f16), torch.empty(batch, inter, **f16)
     norm = torch.ones(hidden, **f16)
     ctx = torch.full((batch,), ctx0, dtype=torch.int32, device=dev)
-    rows = torch.arange(batch, device=dev, dtype=torch.int64) * bps
+
+    lens = torch.empty(batch, dtype=torch.int32, device=dev)
 
     def step():
         xa.copy_(embed)  # each step's new tokens (synthetic embeddings)
-        pos = ctx.clone()
-        slots = tflat[rows + (pos // block_size).to(torch.int64)] * block_size + \
-            (pos % block_size).to(torch.int64)
-        lens = pos + 1
         xin, xout = xa, xb
         for li in range(layers):
             w = lay[li]
             attention_forward_qkv_stage_v2_py(norm, 1e-5, w["q_proj"], w["k_proj"], w["v_proj"],
                                               rms, q, k, v, None, xin, 0, 0, 0, 1, batch)
-            attention_forward_rope_stage_v2_py(q, k, sin, cos, 1, batch, heads, heads, hd, -1, pos)
-            holders[li].kv_tensor_to_slots_with_convert(k.view(batch, heads, hd),
-                                                        v.view(batch, heads, hd), slots)
+            # RoPE on q and k at position ctx, k and v to their cache slots,
+            # lens = ctx + 1: one launch
+            holders[li].rope_and_cache(q.view(batch, heads, hd), k.view(batch, heads, hd),
+                                       v.view(batch, heads, hd), sin, cos, ctx, tables, lens)
             o = att.forward(q.view(batch, heads, hd), max_ctx, lens, tables, holders[li])
             decoder_after_stage_v2_py(w["o_proj"], w["gate_proj"], w["up_proj"], w["down_proj"],
                                       norm, 1e-5, o.view(batch, hidden), xin, x2, rms, hbuf, ubuf,
@@ -217,8 +213,9 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
             "weight_bytes": wbytes, "mean_kv_bytes_per_step": int(kv_bytes),
             "hbm_gbs": round((wbytes + kv_bytes) / (ms * 1e-3) / 1e9, 1), "finite": finite,
             "workload": ("8 Llama-2-7B decoder layers (GPTQ g128 asymmetric), per layer: "
-                         "RMSNorm+q/k/v, RoPE, KV-cache write, paged attention (32 heads x 128, "
-                         "fp16 KV), o_proj+residual, RMSNorm, gate/up+SiLU*mul, down+residual")}
+                         "RMSNorm+q/k/v (one launch), RoPE+KV-cache write (one launch), paged "
+                         "attention (32 heads x 128, fp16 KV), o_proj+residual, RMSNorm, "
+                         "gate/up+SiLU*mul (one launch), down+residual")}
 
 
 def cpu_baseline(seconds: float) -> dict:

@@ -412,7 +412,75 @@ __global__ void rope_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict
   xr[c + half] = h_bits(__builtin_fmaf16(r, cr, rs));
 }
 
+// One decode token per sequence: its q and k rows rotated in place (the
+// arithmetic of rope_kernel, position p = positions[t]), the rotated k row
+// and the v row written to slot block_tables[t][p / bs] * bs + p % bs, and
+// p + 1 stored to lens_out[t] (if given) -- rope on q and k, then
+// reshape_and_cache, in one launch.  A position outside the block table
+// writes no slot; one outside the sin/cos tables leaves q and k unrotated.
+// Grid: (sequence, head slot) with head slots [0, heads) the q heads, then
+// the kv heads (rotate k, write k and v to the slot); 64 threads, one
+// (l, r) pair (or two v elements) each, so no thread loops.
+__global__ void __launch_bounds__(64)
+rope_cache_kernel(uint16_t* __restrict__ q, int64_t q_stride, uint16_t* __restrict__ k,
+                  int64_t k_stride, const uint16_t* __restrict__ v, int64_t v_stride,
+                  const uint16_t* __restrict__ sinp, const uint16_t* __restrict__ cosp,
+                  int max_pos, const int32_t* __restrict__ positions,
+                  const int32_t* __restrict__ block_tables, int max_blocks,
+                  const int64_t* __restrict__ kptr, const int64_t* __restrict__ vptr,
+                  int kv_head_stride, int32_t* __restrict__ lens_out, int heads, int kv_heads,
+                  int hd, int bs) {
+  const int t = blockIdx.x, slot = blockIdx.y, tid = threadIdx.x;
+  const int p = positions[t];
+  if (lens_out != nullptr && slot == 0 && tid == 0) lens_out[t] = p + 1;
+  const int half = hd / 2;
+  const bool rot = p >= 0 && p < max_pos;
+  const bool store = p >= 0 && p / bs < max_blocks;
+  const bool is_q = slot < heads;
+  const int h = is_q ? slot : slot - heads;
+  uint16_t* row = is_q ? q + t * q_stride + h * hd : k + t * k_stride + h * hd;
+  const uint16_t* sr = sinp + (int64_t)(rot ? p : 0) * hd;
+  const uint16_t* cr = cosp + (int64_t)(rot ? p : 0) * hd;
+  uint16_t* kh = nullptr;
+  uint16_t* vh = nullptr;
+  int off = 0;
+  if (!is_q && store) {
+    const int blk = block_tables[(int64_t)t * max_blocks + p / bs];
+    kh = reinterpret_cast<uint16_t*>(kptr[blk]) + (size_t)h * kv_head_stride;
+    vh = reinterpret_cast<uint16_t*>(vptr[blk]) + (size_t)h * kv_head_stride;
+    off = p % bs;
+  }
+  for (int c = tid; c < half; c += 64) {
+    _Float16 l = as_h(row[c]), r = as_h(row[c + half]);
+    if (rot) {
+      const _Float16 ls = r * (_Float16)(-as_h(sr[c]));
+      const _Float16 rs = l * as_h(sr[c + half]);
+      l = __builtin_fmaf16(l, as_h(cr[c]), ls);
+      r = __builtin_fmaf16(r, as_h(cr[c + half]), rs);
+      row[c] = h_bits(l);
+      row[c + half] = h_bits(r);
+    }
+    if (kh != nullptr) {
+      kh[((c / 8) * bs + off) * 8 + c % 8] = h_bits(l);
+      kh[(((c + half) / 8) * bs + off) * 8 + (c + half) % 8] = h_bits(r);
+    }
+  }
+  if (vh != nullptr) {
+    const uint16_t* vr = v + t * v_stride + h * hd;
+    for (int d = tid; d < hd; d += 64) vh[(size_t)d * bs + off] = vr[d];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_rope_cache(const RopeCacheArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.num_seqs, (unsigned)(a.heads + a.kv_heads));
+  rope_cache_kernel<<<grid, 64, 0, stream>>>(
+      a.q, a.q_stride, a.k, a.k_stride, a.v, a.v_stride, a.sinp, a.cosp, a.max_pos, a.positions,
+      a.block_tables, a.max_blocks, a.kptr, a.vptr, a.kv_head_stride, a.lens_out, a.heads,
+      a.kv_heads, a.hd, a.bs);
+  return hipGetLastError();
+}
 
 hipError_t launch_rope(uint16_t* x, const uint16_t* sinp, const uint16_t* cosp, int batch,
                        int rows, int hd, int heads, int max_pos, int past_len,

@@ -421,6 +421,50 @@ int dw4_rope(int batch_size, int rows_per_batch, int num_heads, int head_dim, ui
                                     static_cast<hipStream_t>(stream)));
 }
 
+int dw4_rope_and_cache(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                       int block_size, uint16_t* q, int64_t q_stride, uint16_t* k,
+                       int64_t k_stride, const uint16_t* v, int64_t v_stride,
+                       const uint16_t* sin_table, const uint16_t* cos_table, int max_positions,
+                       const int32_t* positions, const int32_t* block_tables,
+                       int max_blocks_per_seq, const int64_t* key_block_ptrs,
+                       const int64_t* value_block_ptrs, int kv_head_stride,
+                       int32_t* context_lens_out, void* stream) {
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_positions < 0 ||
+      max_blocks_per_seq <= 0)
+    return DW4_ERR_INVALID_ARG;
+  if (head_dim % 8 != 0 || (block_size != 16 && block_size != 32)) return DW4_ERR_UNSUPPORTED;
+  if (num_seqs == 0) return DW4_OK;
+  if (!q || !k || !v || !sin_table || !cos_table || !positions || !block_tables ||
+      !key_block_ptrs || !value_block_ptrs)
+    return DW4_ERR_INVALID_ARG;
+  if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
+      v_stride < (int64_t)num_kv_heads * head_dim || kv_head_stride < block_size * head_dim)
+    return DW4_ERR_INVALID_ARG;
+  dw4::RopeCacheArgs a;
+  a.num_seqs = num_seqs;
+  a.heads = num_heads;
+  a.kv_heads = num_kv_heads;
+  a.hd = head_dim;
+  a.bs = block_size;
+  a.q = q;
+  a.q_stride = q_stride;
+  a.k = k;
+  a.k_stride = k_stride;
+  a.v = v;
+  a.v_stride = v_stride;
+  a.sinp = sin_table;
+  a.cosp = cos_table;
+  a.max_pos = max_positions;
+  a.positions = positions;
+  a.block_tables = block_tables;
+  a.max_blocks = max_blocks_per_seq;
+  a.kptr = key_block_ptrs;
+  a.vptr = value_block_ptrs;
+  a.kv_head_stride = kv_head_stride;
+  a.lens_out = context_lens_out;
+  return status_of(dw4::launch_rope_cache(a, static_cast<hipStream_t>(stream)));
+}
+
 int dw4_gemm_t_workspace_size(int m, int k, int n, int group_size, size_t* workspace_bytes) {
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;

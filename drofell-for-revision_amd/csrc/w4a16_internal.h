@@ -243,4 +243,26 @@ hipError_t launch_rope(uint16_t* x, const uint16_t* sinp, const uint16_t* cosp, 
                        int rows, int hd, int heads, int max_pos, int past_len,
                        const int32_t* past_lens, hipStream_t stream);
 
+// Decode-step rotary embedding of q and k plus the KV-cache write, one launch.
+struct RopeCacheArgs {
+  int num_seqs, heads, kv_heads, hd, bs;
+  uint16_t* q;
+  int64_t q_stride;
+  uint16_t* k;
+  int64_t k_stride;
+  const uint16_t* v;
+  int64_t v_stride;
+  const uint16_t* sinp;
+  const uint16_t* cosp;
+  int max_pos;
+  const int32_t* positions;
+  const int32_t* block_tables;
+  int max_blocks;
+  const int64_t* kptr;
+  const int64_t* vptr;
+  int kv_head_stride;
+  int32_t* lens_out;
+};
+hipError_t launch_rope_cache(const RopeCacheArgs& a, hipStream_t stream);
+
 }  // namespace dw4

@@ -1631,9 +1631,18 @@ hipError_t launch_silu_mul(const uint16_t* g, int64_t ldg, const uint16_t* u, in
 
 // One 256-thread workgroup per row: fp32 sum of squares of the row (inputs
 // clamped to the finite fp16 range, as the reference does), each thread over
-// its 8-element units, then a fixed butterfly within each wave and a fixed
-// order across the four waves; r = 1 / sqrt(sum / k + eps);
-// y = fp16((x * w) * r).  k % 8 == 0, rows 16-byte aligned.
+// its 8-element units in ascending order, then a fixed butterfly within each
+// wave and a fixed order across the four waves; r = 1 / sqrt(sum / k + eps);
+// y = fp16((x * w) * r).  k % 8 == 0, rows 16-byte aligned.  The first
+// kRmsRegUnits units of each thread (rows up to 8192 elements) and their
+// weights are loaded once, all before the first add, and reused for the
+// output; longer rows reload the rest.
+constexpr int kRmsRegUnits = 4;
+
+__device__ __forceinline__ float clamp_h(_Float16 v) {
+  return fmaxf(-65504.0f, fminf((float)v, 65504.0f));
+}
+
 __global__ void __launch_bounds__(256)
 rms_norm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ w,
                 float eps, uint16_t* __restrict__ y, int64_t ldy, int k) {
@@ -1643,12 +1652,31 @@ rms_norm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __r
   const h8* wr = reinterpret_cast<const h8*>(w);
   h8* yr = reinterpret_cast<h8*>(y + (size_t)blockIdx.x * ldy);
   const int units = k / 8;
+  h8 xv[kRmsRegUnits], wv[kRmsRegUnits];
+#pragma unroll
+  for (int i = 0; i < kRmsRegUnits; ++i) {
+    const int u = tid + 256 * i;
+    if (u < units) {
+      xv[i] = xr[u];
+      wv[i] = wr[u];
+    }
+  }
   float sum = 0.f;
-  for (int u = tid; u < units; u += 256) {
+#pragma unroll
+  for (int i = 0; i < kRmsRegUnits; ++i) {
+    if (tid + 256 * i < units) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = clamp_h(xv[i][e]);
+        sum = fmaf(f, f, sum);
+      }
+    }
+  }
+  for (int u = tid + 256 * kRmsRegUnits; u < units; u += 256) {
     const h8 v = xr[u];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float f = fmaxf(-65504.0f, fminf((float)v[e], 65504.0f));
+      const float f = clamp_h(v[e]);
       sum = fmaf(f, f, sum);
     }
   }
@@ -1658,17 +1686,18 @@ rms_norm_kernel(const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __r
   __syncthreads();
   const float total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
   const float r = 1.0f / sqrtf(total / (float)k + eps);
-  for (int u = tid; u < units; u += 256) {
-    const h8 v = xr[u];
-    const h8 wv = wr[u];
+  auto out = [&](h8 v, h8 ww) {
     h8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = fmaxf(-65504.0f, fminf((float)v[e], 65504.0f));
-      o[e] = (_Float16)(f * (float)wv[e] * r);
-    }
-    yr[u] = o;
+    for (int e = 0; e < 8; ++e) o[e] = (_Float16)(clamp_h(v[e]) * (float)ww[e] * r);
+    return o;
+  };
+#pragma unroll
+  for (int i = 0; i < kRmsRegUnits; ++i) {
+    const int u = tid + 256 * i;
+    if (u < units) yr[u] = out(xv[i], wv[i]);
   }
+  for (int u = tid + 256 * kRmsRegUnits; u < units; u += 256) yr[u] = out(xr[u], wr[u]);
 }
 
 hipError_t launch_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps,

@@ -74,6 +74,9 @@ SIGNATURES = {
                                                       _c.POINTER(_c.c_size_t)]),
     "dw4_rope": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _c.c_int,
                             _c.c_int, _P, _P]),
+    "dw4_rope_and_cache": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _P,
+                                      _c.c_int64, _P, _c.c_int64, _P, _c.c_int64, _P, _P,
+                                      _c.c_int, _P, _P, _c.c_int, _P, _P, _c.c_int, _P, _P]),
     "dw4_gemm_group": (_c.c_int, [_c.c_int, _IP, _c.c_int, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_silu_mul": (_c.c_int, [_c.c_int, _P, _c.c_int64, _IP, _IP, _P, _c.c_int64,
                                      _P, _c.c_size_t, _P]),
@@ -87,7 +90,7 @@ SIGNATURES = {
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -90,6 +90,38 @@ class LayerBlocksHolder:
         self.kv_tensor_from_slots_with_convert(k, v, slot_mapping)
         return k, v
 
+    def rope_and_cache(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       sin: torch.Tensor, cos: torch.Tensor, positions: torch.Tensor,
+                       block_tables: torch.Tensor,
+                       context_lens_out: Optional[torch.Tensor] = None) -> None:
+        """One decode token per sequence: rotary embedding of q
+        [seqs, heads, hd] and k [seqs, kv_heads, hd] in place at
+        ``positions`` (int32 [seqs]), the rotated k and v written to their
+        slots through ``block_tables``, and ``positions + 1`` into
+        ``context_lens_out`` -- the reference's rope stage,
+        ``kv_tensor_to_slots_with_convert`` and context-length update in one
+        launch (``dw4_rope_and_cache``)."""
+        seqs, heads, hd = q.shape
+        kvh = k.shape[1]
+        if k.shape != v.shape or k.shape[0] != seqs or hd != self.block_info.head_dim or \
+                kvh != self.block_info.num_key_value_heads:
+            raise AssertionError("q/k/v shapes do not match the block geometry")
+        for t in (q, k, v, sin, cos):
+            if t.dtype != torch.float16 or not t.is_contiguous():
+                raise TypeError("q, k, v, sin, cos must be contiguous fp16")
+        if context_lens_out is not None and (context_lens_out.dtype != torch.int32 or
+                                             context_lens_out.numel() < seqs):
+            raise TypeError("context_lens_out must be int32 with one entry per sequence")
+        pos = positions.to(torch.int32).contiguous()
+        tables = block_tables.to(torch.int32).contiguous()
+        _lib.call("dw4_rope_and_cache", seqs, heads, kvh, hd, flags.BLOCK_SIZE, q.data_ptr(),
+                  q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
+                  sin.data_ptr(), cos.data_ptr(), sin.shape[0], pos.data_ptr(), tables.data_ptr(),
+                  tables.shape[1], self.layer_key_ptr_table_device.data_ptr(),
+                  self.layer_val_ptr_table_device.data_ptr(), self.block_info.head_stride,
+                  None if context_lens_out is None else context_lens_out.data_ptr(),
+                  _stream(self.device))
+
     @staticmethod
     def create_contigious_cacher(block_info: BlockInfo, num_blocks: int, device: torch.device,
                                  dtype: torch.dtype = torch.float16) -> "LayerBlocksHolder":

@@ -97,7 +97,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 6
+#define DW4_ABI_VERSION 7
 
 enum {
   DW4_OK = 0,
@@ -335,6 +335,25 @@ int dw4_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_h
 int dw4_rope(int batch_size, int rows_per_batch, int num_heads, int head_dim, uint16_t* x,
              const uint16_t* sin_table, const uint16_t* cos_table, int max_positions, int past_len,
              const int32_t* past_lens, void* stream);
+
+/* One decode token per sequence: dw4_rope on its q and k rows (position
+ * positions[s]), then dw4_reshape_and_cache of the rotated k and of v into
+ * slot block_tables[s][p / block_size] * block_size + p % block_size, and
+ * context_lens_out[s] = p + 1 (if not NULL) -- three reference calls
+ * (rope.cu, cache_kernels.cu:242-285 and the context-length update of the
+ * decode loop) in one launch.  q [num_seqs][num_heads][head_dim],
+ * k, v [num_seqs][num_kv_heads][head_dim] fp16 with per-sequence strides.
+ * A position outside the block table writes no slot; one outside the
+ * sin/cos tables leaves the rows unrotated.  No counterpart in the
+ * reference as a single call. */
+int dw4_rope_and_cache(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                       int block_size, uint16_t* q, int64_t q_stride, uint16_t* k,
+                       int64_t k_stride, const uint16_t* v, int64_t v_stride,
+                       const uint16_t* sin_table, const uint16_t* cos_table, int max_positions,
+                       const int32_t* positions, const int32_t* block_tables,
+                       int max_blocks_per_seq, const int64_t* key_block_ptrs,
+                       const int64_t* value_block_ptrs, int kv_head_stride,
+                       int32_t* context_lens_out, void* stream);
 
 #ifdef __cplusplus
 }

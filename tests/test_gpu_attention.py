@@ -216,3 +216,41 @@ def test_rope_bit_exact(hip_device, past):
     kr = A.rope(k, sin, cos, kvh, past, lens)
     assert np.array_equal(qd.cpu().numpy().view(np.uint16), qr.view(np.uint16))
     assert np.array_equal(kd.cpu().numpy().view(np.uint16), kr.view(np.uint16))
+
+
+def test_rope_and_cache_bit_exact(hip_device):
+    """The fused decode-step op equals rope on q and k, reshape_and_cache of
+    the rotated k and of v, and context lengths = positions + 1."""
+    bs, heads, kvh, hd = flags.BLOCK_SIZE, 8, 4, 128
+    seqs, nblocks, mb = 5, 20, 4
+    info = BlockInfo(head_dim=hd, num_key_value_heads=kvh)
+    holder = LayerBlocksHolder.create_contigious_cacher(info, nblocks, hip_device)
+    kt, vt = holder.contigious_kv_tenosr
+    kt.zero_()
+    vt.zero_()
+    rng = np.random.default_rng(31)
+    sin, cos = A.rope_tables(3 * bs, hd)
+    q = (rng.standard_normal((seqs, heads, hd)) * 2).astype(np.float16)
+    k = (rng.standard_normal((seqs, kvh, hd)) * 2).astype(np.float16)
+    v = rng.standard_normal((seqs, kvh, hd)).astype(np.float16)
+    # the fourth position is past the sin/cos table, the fifth past the block table
+    pos = np.array([0, 7, bs + 3, 3 * bs + 1, mb * bs + 2], np.int32)
+    tables = rng.permutation(nblocks)[:seqs * mb].reshape(seqs, mb).astype(np.int32)
+    lens = torch.full((seqs,), -7, dtype=torch.int32, device=hip_device)
+    qd, kd, vd = (torch.from_numpy(a).to(hip_device) for a in (q, k, v))
+    say("rope_and_cache")
+    holder.rope_and_cache(qd, kd, vd, torch.from_numpy(sin).to(hip_device),
+                          torch.from_numpy(cos).to(hip_device), torch.from_numpy(pos).to(hip_device),
+                          torch.from_numpy(tables).to(hip_device), lens)
+    torch.cuda.synchronize()
+    q_ref = A.rope(q.reshape(seqs, 1 * heads, hd), sin, cos, heads, -1, pos).reshape(q.shape)
+    k_ref = A.rope(k.reshape(seqs, 1 * kvh, hd), sin, cos, kvh, -1, pos).reshape(k.shape)
+    kc, vc = A.empty_cache(nblocks, kvh, hd, bs, fill=0.0)
+    slots = np.array([tables[s, p // bs] * bs + p % bs if p // bs < mb else -1
+                      for s, p in enumerate(pos)], np.int64)
+    A.reshape_and_cache(k_ref, v, kc, vc, slots)
+    assert np.array_equal(qd.cpu().numpy().view(np.uint16), q_ref.view(np.uint16))
+    assert np.array_equal(kd.cpu().numpy().view(np.uint16), k_ref.view(np.uint16))
+    assert np.array_equal(kt.cpu().numpy().view(np.uint16), kc.view(np.uint16))
+    assert np.array_equal(vt.cpu().numpy().view(np.uint16), vc.view(np.uint16))
+    assert lens.cpu().tolist() == (pos + 1).tolist()
