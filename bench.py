@@ -246,6 +246,50 @@ def cpu_baseline(seconds: float) -> dict:
                        f"median {med * 1e3:.1f} ms; torch {torch.__version__}")}
 
 
+def time_transpose(mats, m: int, steps: int, warmup: int, dev, dense: bool = False) -> float:
+    """ms per pass of the PEFT-backward product g @ W^T over `mats` at M=m:
+    the packed kernel, or (dense=True) the reference's route: bit-exact
+    dequantisation into the shared fp16 buffer, then a library GEMM."""
+    import torch
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(m + 7)
+    gs = {n: torch.randn(m, n, device=dev, generator=gen).to(torch.float16)
+          for n in sorted({t[2] for t in mats})}
+    for _, k, n, q4 in mats:  # size the workspaces before capture
+        q4._transpose_native(gs[n], None)
+        if dense:
+            q4._dense_weight(None)
+
+    def one_pass():
+        for _, k, n, q4 in mats:
+            if dense:
+                torch.matmul(gs[n], q4._dense_weight(None).t())
+            else:
+                q4._transpose_native(gs[n], None)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        one_pass()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one_pass()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize(dev)
+    return start.elapsed_time(end) / steps
+
+
 def sweep(mats, dev, steps: int, warmup: int,
           shapes=((4096, 4096), (4096, 11008), (11008, 4096))) -> None:
     from gptq_synth import algorithmic_bytes, flops
@@ -277,6 +321,8 @@ def main() -> int:
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the M=--prefill-m leg (for hardware-counter passes)")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
+    ap.add_argument("--no-transpose", action="store_true",
+                    help="skip the transposed (PEFT backward) leg")
     ap.add_argument("--no-stage", action="store_true",
                     help="skip the decoder-stage leg (GEMMs + RoPE + KV cache + paged attention)")
     ap.add_argument("--stage-batch", type=int, default=8)
@@ -379,6 +425,22 @@ def main() -> int:
 
     if args.sweep:
         sweep(mats, dev, max(5, args.steps // 5), 3)
+
+    if not args.no_transpose:
+        # PEFT backward through the same 56 frozen matrices at M=16
+        m = 16
+        tms = time_transpose(mats, m, max(5, args.steps // 5), 3, dev)
+        dms = time_transpose(mats, m, max(5, args.steps // 5), 3, dev, dense=True)
+        tbytes = sum(algorithmic_bytes(m, k, n, GROUP, False) for _, k, n, _ in mats)
+        tg = tbytes / (tms * 1e-3) / 1e9
+        log(f"transposed M={m}: {tms * 1e3:.1f} us per step packed, {dms * 1e3:.1f} us "
+            f"dequantise + dense, {tg:.1f} GB/s")
+        result["transpose"] = {"m": m, "value": round(tg, 2), "unit": "GB/s",
+                               "ms_per_step": round(tms, 5), "frac": round(tg / HBM_PEAK_GBS, 4),
+                               "dense_route_ms_per_step": round(dms, 5),
+                               "kernel": "dw4::gemm_t_kernel",
+                               "workload": "g @ W^T (the activation gradient) through the 56 "
+                                           "matrices of the decode leg at M=16"}
 
     if not args.no_merged:
         # Same weight bytes with q/k/v and gate/up merged (4 GEMMs per layer),
