@@ -113,7 +113,8 @@ constexpr int kLdx = kChunkK + 8;  // halfs per staged activation row (16-byte p
 template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
-              float* __restrict__ part, int K, int gs, int G, int cps) {
+              float* __restrict__ part, int K, int gs, int G, int cps, uint32_t mmag,
+              uint32_t gmag) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
   const int item = GRP ? item_of(d, blockIdx.x) : 0;
@@ -154,18 +155,17 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   // group size >= 128: a chunk's scale and zero words travel with its
   // weights in the ring (no staging); smaller groups stage their records
   const int munits = G128 ? 0 : nch * rec;
+  // Unit u = ((i * M + m) * 16 + q): 16-byte piece q of row m of the wave's
+  // i-th chunk.  i = (u >> 4) / M by the host's multiplier (no division in
+  // the kernel: an integer divide is ~25 instructions ahead of every load).
   auto x_unit = [&](int u) -> h8 {
-    const int i = u / xupc;
-    const int r = u - i * xupc;
-    const int m = r >> 4;
-    const int k = (c0 + wave + i * WAVES) * kChunkK + (r & 15) * 8;
+    const uint32_t v = (uint32_t)u >> 4;
+    const int i = M == 1 ? (int)v : (int)__umulhi(v, mmag);
+    const int m = (int)v - i * M;
+    const int k = (c0 + wave + i * WAVES) * kChunkK + (u & 15) * 8;
     return load_x_unit<ACT>(x + (size_t)m * ldx, perm, k);
   };
-  auto x_dst = [&](int u) -> _Float16* {
-    const int i = u / xupc;
-    const int r = u - i * xupc;
-    return xw + ((size_t)i * M + (r >> 4)) * kLdx + (r & 15) * 8;
-  };
+  auto x_dst = [&](int u) -> _Float16* { return xw + (size_t)(u >> 4) * kLdx + (u & 15) * 8; };
   auto m_word = [&](int v) -> uint32_t {
     const int i = v / rec;
     const int r = v - i * rec;
@@ -199,7 +199,9 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
     const int c = wave + i * WAVES;
     q = __builtin_nontemporal_load(qp + (size_t)c * 64);
     if (G128) {
-      const int g = ((c0 + c) * kChunkK) / gs;
+      // group of chunk c0 + c: the chunk itself for 128-row groups, else the
+      // host's multiplier for chunks per group
+      const int g = gmag == 0 ? c0 + c : (int)__umulhi((uint32_t)(c0 + c), gmag);
       sw = sp[(size_t)g * 8];
       zw = zp[(size_t)g * 2];
     }
@@ -1406,6 +1408,13 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
   return hipGetLastError();
 }
 
+// ceil(2^32 / d) for d >= 2 (0 for d = 1): floor(n / d) = umulhi(n, magic)
+// exactly while n * d < 2^32 (the rounding excess of the magic, below one,
+// then adds less than 1/d to n/d).  Chunk and row counts stay far below that.
+static uint32_t div_magic(int d) {
+  return d <= 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
 template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP>
 static hipError_t launch_decode_one(const GemmArgs& a, const Items& d, const DecodePlan& p,
                                     float* part, hipStream_t stream) {
@@ -1421,7 +1430,8 @@ static hipError_t launch_decode_one(const GemmArgs& a, const Items& d, const Dec
     }
   }
   decode_kernel<MT, WAVES, U, G128, ACT, GRP><<<grid, WAVES * 64, p.smem, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, d, part, a.K, a.gs, a.G, p.cps);
+      (const _Float16*)a.x, a.ldx, a.M, d, part, a.K, a.gs, a.G, p.cps, div_magic(a.M),
+      G128 && a.gs > kChunkK ? div_magic(a.gs / kChunkK) : 0u);
   return hipGetLastError();
 }
 
