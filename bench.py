@@ -38,7 +38,7 @@ def log(msg: str) -> None:
 
 
 def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None,
-                   scale_mul: float = 0.01):
+                   scale_mul: float = 0.01, act_order: bool = False):
     import torch
     from gptq_synth import LLAMA2_7B_SHAPES
     from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
@@ -58,16 +58,20 @@ def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None,
                                    device=dev, generator=gen)
             scales = (torch.randn(groups, n, device=dev, generator=gen).abs() * scale_mul
                       + scale_mul / 10).to(torch.float16)
-            q4 = Q4MatrixV2(qweight, qzeros, scales, k, n, None, False, tp, cache)
+            g_idx = None
+            if act_order:  # config 4: g_idx[k] = pi(k) // 128 for a seeded permutation pi
+                g_idx = (torch.randperm(k, device=dev, generator=gen) // GROUP).to(torch.int32)
+            q4 = Q4MatrixV2(qweight, qzeros, scales, k, n, g_idx, act_order, tp, cache)
             mats.append((name, k, n, q4))
-            del qweight, qzeros, scales
+            del qweight, qzeros, scales, g_idx
     cache.init_cache()
     torch.cuda.synchronize()
     return mats, cache
 
 
-def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None):
-    """Capture one pass over `mats` at M=m into a graph; return ms per pass."""
+def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None, per_replay=None):
+    """Capture one pass over `mats` at M=m into a graph; return ms per pass.
+    With a list `per_replay`, each replay is also timed on its own (appended, ms)."""
     import torch
 
     sel = [t for t in mats if select is None or select(t)]
@@ -104,6 +108,15 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None):
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / steps
+    if per_replay is not None:
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(steps)]
+        for a, b in evs:
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+        torch.cuda.synchronize(dev)
+        per_replay.extend(a.elapsed_time(b) for a, b in evs)
     return ms, wall, sel
 
 
@@ -291,19 +304,32 @@ def time_transpose(mats, m: int, steps: int, warmup: int, dev, dense: bool = Fal
 
 
 def sweep(mats, dev, steps: int, warmup: int,
-          shapes=((4096, 4096), (4096, 11008), (11008, 4096))) -> None:
+          shapes=((4096, 4096), (4096, 11008), (11008, 4096)),
+          ms_list=(1, 2, 4, 8, 16, 64, 256, 1024, 2048), act_order: bool = False,
+          tag: str = "") -> None:
+    """Per-shape, per-M lines (JSON on stderr): mean per launch over the
+    rotated matrices of that shape, and the median / p10 / p90 of single
+    graph replays (each replay = one launch per matrix of the shape)."""
     from gptq_synth import algorithmic_bytes, flops
     for (k, n) in shapes:
-        for m in (1, 2, 4, 8, 16, 64, 256, 1024):
+        for m in ms_list:
+            reps = []
             ms, _, sel = time_graph(mats, m, steps, warmup, dev,
-                                    select=lambda t, k=k, n=n: t[1] == k and t[2] == n)
+                                    select=lambda t, k=k, n=n: t[1] == k and t[2] == n,
+                                    per_replay=reps)
             per = ms / len(sel) * 1e3
-            b = algorithmic_bytes(m, k, n, GROUP, False)
+            q = sorted(r / len(sel) * 1e3 for r in reps)
+            pct = lambda f: round(q[min(len(q) - 1, int(f * len(q)))], 3)
+            b = algorithmic_bytes(m, k, n, GROUP, act_order)
             f = flops(m, k, n)
-            log(json.dumps({"shape": f"{k}x{n}", "m": m, "us": round(per, 3),
+            bound = "hbm" if b / HBM_PEAK_GBS * 1e-3 >= f / MFMA_FP16_PEAK_TFLOPS * 1e-6 else "mfma"
+            frac = (b / per / 1e3 / HBM_PEAK_GBS) if bound == "hbm" else \
+                (f / per / 1e6 / MFMA_FP16_PEAK_TFLOPS)
+            log(json.dumps({"config": tag, "shape": f"{k}x{n}", "m": m, "act_order": act_order,
+                            "matrices": len(sel), "us": round(per, 3), "median_us": pct(0.5),
+                            "p10_us": pct(0.1), "p90_us": pct(0.9),
                             "GB/s": round(b / per / 1e3, 1), "TFLOP/s": round(f / per / 1e6, 2),
-                            "hbm_frac": round(b / per / 1e3 / HBM_PEAK_GBS, 4),
-                            "mfma_frac": round(f / per / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)}))
+                            "bound": bound, "frac": round(frac, 4)}))
 
 
 def main() -> int:
@@ -353,7 +379,7 @@ def main() -> int:
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
     log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
-    mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1024 if args.sweep else 1))
+    mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1))
     weight_bytes = sum(q4.qweight.numel() * 4 + q4.scales.numel() * 2 + q4.qzeros.numel() * 4
                        for _, _, _, q4 in mats)
 
@@ -424,7 +450,22 @@ def main() -> int:
                              "peak": MFMA_FP16_PEAK_TFLOPS, "bound": "mfma"}
 
     if args.sweep:
-        sweep(mats, dev, max(5, args.steps // 5), 3)
+        # each shape rotates over distinct matrices totalling >= 512 MB, so the
+        # 256 MB Infinity Cache cannot serve the weights between launches
+        plan = [((4096, 4096), False, (1, 2, 4, 8, 16, 64, 256, 1024, 2048), "C2/C3 (7B)"),
+                ((4096, 11008), False, (1, 2, 4, 8, 16, 64, 256, 1024, 2048), "C2/C3 (7B)"),
+                ((11008, 4096), False, (1, 2, 4, 8, 16, 64, 256, 1024, 2048), "C2/C3 (7B)"),
+                ((5120, 5120), True, (1, 8, 64), "C4 (13B act-order)"),
+                ((5120, 13824), True, (1, 8, 64), "C4 (13B act-order)"),
+                ((13824, 5120), True, (1, 8, 64), "C4 (13B act-order)")]
+        for (k, n), act, ms_list, tag in plan:
+            count = -(-(512 << 20) // algorithmic_bytes(1, k, n, GROUP, act))
+            sm, sc = build_matrices(dev, count, max(ms_list), seed0=7000 + k + n,
+                                    shapes={f"{k}x{n}": (k, n)}, act_order=act)
+            sweep(sm, dev, max(5, args.steps // 5), 3, shapes=((k, n),), ms_list=ms_list,
+                  act_order=act, tag=tag)
+            del sm, sc
+            torch.cuda.empty_cache()
 
     if not args.no_transpose:
         # PEFT backward through the same 56 frozen matrices at M=16
@@ -470,7 +511,8 @@ def main() -> int:
         result["merged"] = merged
         if args.sweep:
             sweep(mmats, dev, max(5, args.steps // 5), 3,
-                  shapes=((4096, 12288), (4096, 22016)))
+                  shapes=((4096, 12288), (4096, 22016)), ms_list=(1, 2, 4, 8, 16, 64, 256),
+                  tag="merged (8 layers; q/k/v set 210 MB)")
         del mmats, _mcache
 
     if not args.no_stage:

@@ -98,14 +98,22 @@ bool use_decode(int path, int m, int n) {
   return dw4::auto_decode(m, n, cu_count());
 }
 
-size_t workspace_for(int path, int m, int k, int n, int group_size) {
+// Split-K bytes, then (act-order) the gathered activations: 256-aligned and
+// never over the arrival-counter head, which every call leaves zero for the
+// next split call on the workspace.
+size_t workspace_for(int path, int m, int k, int n, int group_size, bool act) {
   if (m <= 0) return 0;
-  if (use_decode(path, m, n)) {
+  const bool decode = use_decode(path, m, n);
+  size_t split;
+  if (decode) {
     const dw4::DecodePlan p = dw4::plan_decode(m, k, n, group_size, cu_count());
-    return dw4::split_ws_bytes(p.splits, (size_t)m * n);
+    split = dw4::split_ws_bytes(p.splits, (size_t)m * n);
+  } else {
+    const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
+    split = prefill_ws_bytes(p, m, n);
   }
-  const dw4::PrefillPlan p = plan_prefill(m, k, n, 0, 0, false);
-  return prefill_ws_bytes(p, m, n);
+  if (!act) return split;
+  return dw4::gather_offset(split) + dw4::gather_bytes(m, k);
 }
 
 }  // namespace
@@ -143,8 +151,9 @@ int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
     size_t ws = 0;
     // enough for either explicit path at every M up to max_m
     for (int m = 1; m <= max_m; ++m) {
-      ws = std::max(ws, workspace_for(DW4_PATH_PREFILL, m, k, n, group_size));
-      if (m <= dw4::kDecodeMaxM) ws = std::max(ws, workspace_for(DW4_PATH_DECODE, m, k, n, group_size));
+      ws = std::max(ws, workspace_for(DW4_PATH_PREFILL, m, k, n, group_size, act_order != 0));
+      if (m <= dw4::kDecodeMaxM)
+        ws = std::max(ws, workspace_for(DW4_PATH_DECODE, m, k, n, group_size, act_order != 0));
     }
     *workspace_bytes = ws;
   }
@@ -155,8 +164,7 @@ int dw4_workspace_size(int m, int k, int n, int group_size, int act_order, size_
   const int st = check_shape(k, n, group_size);
   if (st != DW4_OK) return st;
   if (m < 0 || workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
-  (void)act_order;  // act-order gathers during staging: no extra workspace
-  *workspace_bytes = workspace_for(DW4_PATH_AUTO, m, k, n, group_size);
+  *workspace_bytes = workspace_for(DW4_PATH_AUTO, m, k, n, group_size, act_order != 0);
   return DW4_OK;
 }
 
@@ -240,20 +248,41 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
   a.res = res;
   a.ldres = ldres;
 
+  // Act-order: where the workspace holds the gathered activations after the
+  // split-K area, gather x into the packed row order once and run the
+  // kernels without perm; otherwise they gather per workgroup (same results).
+  auto gather_after = [&](size_t split_need) -> int {
+    if (perm == nullptr || workspace == nullptr || !aligned16(workspace)) return DW4_OK;
+    const size_t off = dw4::gather_offset(split_need);
+    if (workspace_bytes < off + dw4::gather_bytes(m, k)) return DW4_OK;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(workspace) + off);
+    const int e = status_of(dw4::launch_gather_rows(x, ldx, perm, xs, k, m, s));
+    if (e != DW4_OK) return e;
+    a.x = xs;
+    a.ldx = k;
+    a.perm = nullptr;
+    return DW4_OK;
+  };
+
   if (decode) {
     const dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
     float* part = nullptr;
+    size_t need = 0;
     if (plan.splits > 1) {
-      const size_t need = dw4::split_ws_bytes(plan.splits, (size_t)m * n);
+      need = dw4::split_ws_bytes(plan.splits, (size_t)m * n);
       if (workspace == nullptr || workspace_bytes < need) return DW4_ERR_WORKSPACE;
       if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
       part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + dw4::kWsHeadBytes);
     }
+    const int e = gather_after(need);
+    if (e != DW4_OK) return e;
     return status_of(dw4::launch_decode(a, plan, part, s));
   }
 
   dw4::PrefillPlan plan = plan_prefill(m, k, n, split_k, workspace ? workspace_bytes : 0, true);
   if (plan.splits > 1 && !aligned16(workspace)) plan.splits = 1;
+  const int e = gather_after(plan.splits > 1 ? prefill_ws_bytes(plan, m, n) : 0);
+  if (e != DW4_OK) return e;
   return status_of(dw4::launch_prefill(a, plan, workspace, s));
 }
 

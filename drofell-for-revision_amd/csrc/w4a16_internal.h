@@ -152,6 +152,18 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
                          const int32_t* perm, uint32_t* pq, uint32_t* pz, uint16_t* ps,
                          int K, int N, int G, hipStream_t stream);
 hipError_t launch_decode(const GemmArgs& a, const DecodePlan& p, float* part, hipStream_t stream);
+// xs[m][j] = x[m][perm[j]] for m < M, j < K (K % 8 == 0): x in the packed row order.
+hipError_t launch_gather_rows(const uint16_t* x, int64_t ldx, const int32_t* perm, uint16_t* xs,
+                              int K, int M, hipStream_t stream);
+// Act-order calls gather x into the packed row order first (a workspace
+// buffer of gather_bytes): every workgroup would otherwise gather its own
+// activation slices, 8 two-byte loads at scattered addresses per 16-byte
+// unit behind a dependent load of perm.
+inline size_t gather_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(size_t)255; }
+// Workspace offset of the gathered activations after `split` bytes of
+// split-K area: 256-aligned and past the arrival-counter head (declared
+// below), which must stay zero between calls.
+inline size_t gather_offset(size_t split);
 hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
 // One launch over every strip of g's matrices (decode plan with one split).
 hipError_t launch_decode_group(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
@@ -173,6 +185,10 @@ hipError_t launch_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* w, fl
 // one call never land on the counters of another.
 constexpr int kSplitCounters = 4096;
 constexpr size_t kWsHeadBytes = kSplitCounters * sizeof(int);
+inline size_t gather_offset(size_t split) {
+  const size_t b = split > kWsHeadBytes ? split : kWsHeadBytes;
+  return (b + 255) & ~(size_t)255;
+}
 inline size_t split_ws_bytes(int splits, size_t plane_floats) {
   return splits > 1 ? kWsHeadBytes + (size_t)splits * plane_floats * sizeof(float) : 0;
 }

@@ -78,6 +78,21 @@ __global__ void repack_meta_kernel(const uint16_t* __restrict__ scales,
   if (j < 2) pzeros[sg * 2 + j] = qzeros[(size_t)g * (N / 8) + 2 * s + j];
 }
 
+// xs[m][j] = x[m][perm[j]]: activations in the packed (group-sorted) row
+// order, one 16-byte unit of 8 sorted rows per thread.  Act-order calls with
+// register-fed or MFMA kernels gather once here instead of in every
+// workgroup (each gathered unit is 8 two-byte loads at scattered addresses).
+__global__ void gather_rows_kernel(const _Float16* __restrict__ x, int64_t ldx,
+                                   const int32_t* __restrict__ perm, _Float16* __restrict__ xs,
+                                   int K, int M) {
+  const int upr = K / 8;
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= (int64_t)M * upr) return;
+  const int m = (int)(u / upr);
+  const int j = (int)(u - (int64_t)m * upr) * 8;
+  *(h8*)(xs + (size_t)m * K + j) = load_x_unit<true>(x + (size_t)m * ldx, perm, j);
+}
+
 // ---------------------------------------------------------------------------
 // Per-(strip, group) metadata record as staged in LDS: 8 dwords holding the
 // 16 fp16 scales of the strip's columns, then the 2 dwords of stored zeros.
@@ -1413,6 +1428,14 @@ hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const 
 // then adds less than 1/d to n/d).  Chunk and row counts stay far below that.
 static uint32_t div_magic(int d) {
   return d <= 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
+hipError_t launch_gather_rows(const uint16_t* x, int64_t ldx, const int32_t* perm, uint16_t* xs,
+                              int K, int M, hipStream_t stream) {
+  const int64_t units = (int64_t)M * (K / 8);
+  gather_rows_kernel<<<(unsigned)((units + 255) / 256), 256, 0, stream>>>(
+      reinterpret_cast<const _Float16*>(x), ldx, perm, reinterpret_cast<_Float16*>(xs), K, M);
+  return hipGetLastError();
 }
 
 template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP>

@@ -158,12 +158,21 @@ def test_make_perm_rejects_bad_g_idx():
 def test_workspace_size_rules():
     # M=1 activations fit the decode workgroup's LDS: one split, no workspace
     assert _lib.workspace_size(1, 4096, 4096, 128, False) == 0
-    assert _lib.workspace_size(1, 13824, 5120, 128, True) == 0
-    # act-order gathers while staging: no gather buffer
-    assert _lib.workspace_size(8, 4096, 4096, 128, True) == _lib.workspace_size(8, 4096, 4096, 128, False)
     # M = 5..64 runs the register-fed decode kernel: K is never split
     assert _lib.workspace_size(16, 11008, 4096, 128, False) == 0
-    assert _lib.workspace_size(8, 13824, 5120, 128, True) == 0
+    # act-order gathers x into the packed row order first: M * K fp16
+    # (rounded to 256 bytes) after the 16 KiB arrival-counter head, which
+    # every call leaves zero for the split calls that share the buffer
+    head = 4096 * 4
+    assert _lib.workspace_size(1, 13824, 5120, 128, True) == head + 13824 * 2
+    assert _lib.workspace_size(8, 13824, 5120, 128, True) == head + 8 * 13824 * 2
+    assert _lib.workspace_size(5, 4096, 4096, 128, True) == head + 5 * 4096 * 2
+    # prefill: the gathered activations follow the split-K area (256-aligned)
+    split = _lib.workspace_size(256, 4096, 4096, 128, False)
+    assert _lib.workspace_size(256, 4096, 4096, 128, True) == \
+        (split + 255) // 256 * 256 + 256 * 4096 * 2
+    # the per-matrix query covers every M up to max_m, gather included
+    assert _lib.query_sizes(5120, 13824, 128, True, 64)["workspace"] >= 64 * 5120 * 2
     # the automatic path takes decode up to M = 24, and up to M = 32 when
     # N / 16 <= CUs (256 without a device); above, split-K prefill needs a
     # workspace at these shapes

@@ -188,6 +188,54 @@ def test_act_order_13b(hip_device, kn):
             check_tol(y, gptq.gemm_ref(x.numpy(), w), f"act {k}x{n} M={m} path {path}")
 
 
+def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
+    """Act-order calls gather x into the packed row order in the workspace
+    when it has room, else the kernels gather per workgroup: the two feed the
+    same values to the same sums, so the outputs are bit-identical."""
+    k, n = 5120, 2048
+    lay, w = oracle_w(k, n, 128, 4242, False, True)
+    q4 = build(lay, hip_device)
+    lib = _lib.load()
+    for m, path in ((8, _lib.DW4_PATH_DECODE), (64, _lib.DW4_PATH_DECODE),
+                    (64, _lib.DW4_PATH_PREFILL), (300, _lib.DW4_PATH_PREFILL)):
+        say(f"act-order gather-first vs in-kernel gather M={m} path={path}")
+        x = make_x(m, k, seed=m + 77)
+        xd = x.to(hip_device)
+        outs = []
+        for with_ws in (True, False):
+            ws = torch.zeros(_lib.workspace_size(m, k, n, 128, True) if with_ws else 0,
+                             dtype=torch.uint8, device=hip_device)
+            if with_ws:
+                assert ws.numel() >= m * k * 2  # room for the gathered activations
+            y = torch.empty(m, n, dtype=torch.float16, device=hip_device)
+            st = lib.dw4_gemm_path(path, 1, m, k, n, 128, xd.data_ptr(), k,
+                                   q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
+                                   q4.scales.data_ptr(), q4.perm.data_ptr(), None,
+                                   y.data_ptr(), n, ws.data_ptr() if with_ws else None,
+                                   ws.numel(), torch.cuda.current_stream().cuda_stream)
+            assert st == _lib.DW4_OK, _lib.strerror(st)
+            torch.cuda.synchronize()
+            if with_ws:  # the arrival-counter head stays zero for later split calls
+                assert not ws[:4096 * 4].any(), f"counter head written M={m}"
+            outs.append(y.cpu())
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={m}"
+        ref = gptq.gemm_ref(x.numpy(), w)
+        check_tol(outs[0], ref, f"gather-first M={m} path {path}")
+        if path == _lib.DW4_PATH_PREFILL:  # automatic split: gathered rows after the planes
+            say(f"act-order gather-first after split-K planes M={m}")
+            ws = torch.zeros(_lib.workspace_size(m, k, n, 128, True), dtype=torch.uint8,
+                             device=hip_device)
+            y = torch.empty(m, n, dtype=torch.float16, device=hip_device)
+            st = lib.dw4_gemm_path(path, 0, m, k, n, 128, xd.data_ptr(), k,
+                                   q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
+                                   q4.scales.data_ptr(), q4.perm.data_ptr(), None,
+                                   y.data_ptr(), n, ws.data_ptr(), ws.numel(),
+                                   torch.cuda.current_stream().cuda_stream)
+            assert st == _lib.DW4_OK, _lib.strerror(st)
+            torch.cuda.synchronize()
+            check_tol(y.cpu(), ref, f"gather-first split M={m}")
+
+
 @pytest.mark.parametrize("g", [32, 64, 256, 1024])
 def test_group_sizes(hip_device, g):
     k, n = 1024, 272  # N = 17 strips: a partial prefill N-tile
