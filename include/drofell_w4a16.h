@@ -128,7 +128,10 @@ int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
                     size_t* workspace_bytes);
 
 /* Workspace bytes one dw4_gemm call at exactly this M needs (0 allowed when
- * it returns 0). */
+ * it returns 0).  With act_order it includes M*K fp16 for x gathered into
+ * the packed row order (placed after the split-K area and the arrival
+ * counters); a call whose workspace lacks that room gathers inside every
+ * workgroup instead: the same result bit for bit, slower. */
 int dw4_workspace_size(int m, int k, int n, int group_size, int act_order,
                        size_t* workspace_bytes);
 
