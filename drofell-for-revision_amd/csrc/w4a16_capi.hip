@@ -58,6 +58,24 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
   p.bn = n >= 2048 ? 256 : 128;
   const int kc = k / kChunkK;
   const int cus_now = cu_count();
+  // automatic split count for a tile count (rule below)
+  auto auto_splits = [&](int tiles) {
+    int sp = tiles >= cus_now ? 1 : cus_now / tiles;
+    sp = std::min(sp, std::max(1, kc / 8));
+    return std::min(sp, 8);
+  };
+  auto filled = [&](int bm, int bn) {  // workgroups of one round, at most one per CU
+    const int t = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+    return std::min(cus_now, t * auto_splits(t));
+  };
+  // Mid M (33..128 rows): 128-column tiles, and 32-row tiles where they fill
+  // more CUs than 64-row ones (ties keep the taller tile, which dequantises
+  // each weight fragment for more rows).  Measured at M=64: 4096^2 20.2 ->
+  // 13.4 us, 4096x11008 22.3 -> 19.7, 11008x4096 30.8 -> 24.0.
+  if (p.bm >= 32 && m <= 128) {
+    p.bn = 128;
+    if (p.bm == 64 && m <= 64 && filled(32, 128) > filled(64, 128)) p.bm = 32;
+  }
   // 128-row tiles reuse each dequantised weight fragment twice as often
   // (measured ~44% vs ~33% of a CU's MFMA peak) but halve the tile count:
   // take them wherever 64-row tiles would need more than one round of
@@ -67,16 +85,12 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
     if (((m + 63) / 64) * nt > cus_now && ((m + 127) / 128) * nt <= cus_now) p.bm = 128;
   }
   const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
-  int splits = split_req;
-  if (splits <= 0) {
-    const int cus = cus_now;  // one workgroup per CU at a time
-    splits = tiles >= cus ? 1 : cus / tiles;
-    // at least 8 chunks per split and at most 8 splits: the last split of a
-    // tile to arrive sums all the others' partials, so more splits lengthen
-    // that tail faster than they add parallelism (measured on 7B shapes)
-    splits = std::min(splits, std::max(1, kc / 8));
-    splits = std::min(splits, 8);
-  }
+  // Automatic splits: enough to give every CU a workgroup (one per CU at a
+  // time), with at least 8 chunks per split and at most 8 splits: the last
+  // split of a tile to arrive sums all the others' partials, so more splits
+  // lengthen that tail faster than they add parallelism (measured on 7B
+  // shapes).
+  int splits = split_req > 0 ? split_req : auto_splits(tiles);
   splits = std::max(1, std::min(splits, kc));
   // the launcher rounds to whole chunks per split
   const int cps = (kc + splits - 1) / splits;
