@@ -120,6 +120,187 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None, per_repl
     return ms, wall, sel
 
 
+def time_callable(fn, steps: int, warmup: int, dev) -> float:
+    """ms per call of `fn` (enqueues device work only), captured once into a
+    HIP graph and replayed `steps` times between HIP events."""
+    import torch
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize(dev)
+    del graph
+    return start.elapsed_time(end) / steps
+
+
+# (label, bytes, workgroups, threads): the weight bytes of a decode launch and
+# the decode kernel's launch shape at M=1 (one workgroup per 16-column strip;
+# 16 waves when strips <= CUs, 4 when strips >= 2 x CUs), plus two shapes with
+# more, smaller workgroups for the 8 MiB case.
+STREAM_SHAPES = (
+    ("4096x4096", 8 << 20, 256, 1024),
+    ("4096x4096 1024x256", 8 << 20, 1024, 256),
+    ("4096x4096 2048x256", 8 << 20, 2048, 256),
+    ("4096x11008", 4096 * 11008 // 2, 688, 256),
+    ("11008x4096", 11008 * 4096 // 2, 256, 1024),
+    ("4096x12288", 4096 * 12288 // 2, 768, 256),
+    ("4096x22016", 4096 * 22016 // 2, 1376, 256),
+)
+
+
+def stream_ceiling(dev, steps: int) -> list:
+    """Per-launch time of the library's calibration read (dw4_stream_read)
+    in the decode launch shapes.  Each graph replay reads consecutive slices
+    of a 1 GiB buffer, so no slice is read twice within 1 GiB (four times the
+    Infinity Cache)."""
+    import torch
+    from hip_extends import _lib
+
+    lib = _lib.load()
+    pool_bytes = 1 << 30
+    pool = torch.randint(-2 ** 31, 2 ** 31, (pool_bytes // 4,), dtype=torch.int32, device=dev)
+    sink = torch.zeros(2048 * 1024, dtype=torch.int32, device=dev)
+    out = []
+    for label, nbytes, wgs, threads in STREAM_SHAPES:
+        per = pool_bytes // nbytes
+        stream = torch.cuda.current_stream(dev).cuda_stream
+
+        def one_pass(nbytes=nbytes, wgs=wgs, threads=threads, per=per):
+            st = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(per):
+                _lib.check("dw4_stream_read", lib.dw4_stream_read(
+                    pool.data_ptr() + i * nbytes, nbytes, wgs, threads, 0x9E3779B9,
+                    sink.data_ptr(), st))
+        del stream
+        ms = time_callable(one_pass, max(3, steps // 10), 2, dev)
+        us = ms * 1e3 / per
+        rec = {"shape": label, "bytes": nbytes, "workgroups": wgs, "threads": threads,
+               "us_per_launch": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+               "launches_per_pass": per}
+        log(json.dumps({"stream_read": rec}))
+        out.append(rec)
+    del pool, sink
+    torch.cuda.empty_cache()
+    return out
+
+
+def crossover(mats, dev, steps: int, ms_list=(64, 128, 256, 512, 768, 1024, 2048, 4096, 8192)):
+    """Per M: the 56-matrix pass through the native W4A16 kernel, through the
+    reference's dense route (bit-exact dequantisation into one shared fp16
+    buffer, then a library GEMM per matrix) and through a dense GEMM over an
+    already-reconstructed weight (the PEFT route that keeps the weight)."""
+    import torch
+
+    kmax = max(k * n for _, k, n, _ in mats)
+    temp = torch.empty(kmax, dtype=torch.float16, device=dev)
+    shapes = sorted({(k, n) for _, k, n, _ in mats})
+    kept = {kn: torch.empty(kn, dtype=torch.float16, device=dev) for kn in shapes}
+    for (k, n), w in kept.items():
+        q4 = next(q for _, kk, nn, q in mats if (kk, nn) == (k, n))
+        q4.get_float16_weights_matrix_v2(w)
+    rows = []
+    for m in ms_list:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(m)
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.float16)
+              for k in sorted({k for k, _ in shapes})}
+        ys = {n: torch.empty(m, n, dtype=torch.float16, device=dev)
+              for n in sorted({n for _, n in shapes})}
+
+        def native():
+            for _, k, n, q4 in mats:
+                q4.matmul(xs[k], output=ys[n])
+
+        def dense():
+            for _, k, n, q4 in mats:
+                w = temp[: k * n].view(k, n)
+                q4.get_float16_weights_matrix_v2(w)
+                torch.matmul(xs[k], w, out=ys[n])
+
+        def dense_kept():
+            for _, k, n, q4 in mats:
+                torch.matmul(xs[k], kept[(k, n)], out=ys[n])
+
+        st = max(3, steps // 10)
+        rec = {"m": m, "native_ms": round(time_callable(native, st, 2, dev), 4),
+               "dense_ms": round(time_callable(dense, st, 2, dev), 4),
+               "dense_kept_weight_ms": round(time_callable(dense_kept, st, 2, dev), 4)}
+        log(json.dumps({"crossover": rec}))
+        rows.append(rec)
+        del xs, ys
+        torch.cuda.empty_cache()
+    return rows
+
+
+def stage_reference_fp32(x, layer_mats, norm, eps, kcaches, vcaches, tables, pos, sin, cos,
+                         heads, hd, bs):
+    """One decode step of the stage in float32 torch ops on the GPU, rounded
+    to fp16 where the stage's tensors are fp16: the bench's own check of its
+    stage leg (the weights come from the bit-exact dequantiser; the caches
+    are copies taken before the step and are updated here)."""
+    import torch
+    import torch.nn.functional as F
+
+    def rms_norm(t):
+        t = t.float().clamp(-65504.0, 65504.0)
+        r = torch.rsqrt(t.pow(2).mean(dim=-1, keepdim=True) + eps)
+        return (t * norm.float() * r).half()
+
+    def mm(a, q4):
+        return (a.float() @ q4.get_float16_weights_matrix_v2().float()).half()
+
+    def rope(t):  # t [b, heads, hd] fp16, rotate-half at pos[b]
+        s_, c_ = sin[pos.long()].float()[:, None, :], cos[pos.long()].float()[:, None, :]
+        tf = t.float()
+        rot = torch.cat([-tf[..., hd // 2:], tf[..., :hd // 2]], dim=-1)
+        return (tf * c_ + rot * s_).half()
+
+    b = x.shape[0]
+    ar = torch.arange(b, device=x.device)
+    for li, w in enumerate(layer_mats):
+        h = rms_norm(x)
+        q = rope(mm(h, w["q_proj"]).view(b, heads, hd))
+        k = rope(mm(h, w["k_proj"]).view(b, heads, hd))
+        v = mm(h, w["v_proj"]).view(b, heads, hd)
+        blk = tables[ar, pos.long() // bs].long()
+        off = pos.long() % bs
+        kc, vc = kcaches[li], vcaches[li]  # [blocks, heads, hd/8, bs, 8], [blocks, heads, hd, bs]
+        kc[blk, :, :, off, :] = k.view(b, heads, hd // 8, 8)
+        vc[blk, :, :, off] = v
+        outs = []
+        for s in range(b):
+            n = int(pos[s]) + 1
+            kb = kc[tables[s].long()].permute(0, 3, 1, 2, 4).reshape(-1, heads, hd)[:n]
+            vb = vc[tables[s].long()].permute(0, 3, 1, 2).reshape(-1, heads, hd)[:n]
+            kt = kb.float().permute(1, 2, 0).contiguous()  # [heads, hd, n]
+            logits = torch.bmm(q[s].float().unsqueeze(1), kt) * hd ** -0.5  # [heads, 1, n]
+            vt = vb.float().permute(1, 0, 2).contiguous()  # [heads, n, hd]
+            outs.append(torch.bmm(F.softmax(logits, dim=-1), vt).squeeze(1))
+        attn = torch.stack(outs).half().view(b, heads * hd)
+        x2 = (x.float() + mm(attn, w["o_proj"]).float()).half()
+        h2 = rms_norm(x2)
+        g, u = mm(h2, w["gate_proj"]).float(), mm(h2, w["up_proj"]).float()
+        act = (g / (1.0 + torch.exp(-g)) * u).half()
+        x = (x2.float() + mm(act, w["down_proj"]).float()).half()
+    return x
+
+
 def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_size: int,
               warmup: int) -> dict:
     """The 8-layer Llama-2-7B decoder stage at decode: per layer the fused
@@ -191,12 +372,22 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
             xin, xout = xout, xin
         ctx.add_(1)
 
+    # step 0 on fresh state, checked against the float32 composition
+    kref = [h.contigious_kv_tenosr[0].clone() for h in holders]
+    vref = [h.contigious_kv_tenosr[1].clone() for h in holders]
+    pos0 = ctx.clone()
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
         step()
     torch.cuda.current_stream(dev).wait_stream(side)
     torch.cuda.synchronize(dev)
+    got = (xa if layers % 2 == 0 else xb).float()
+    want = stage_reference_fp32(embed, lay, norm, 1e-5, kref, vref, tables, pos0, sin, cos,
+                                heads, hd, block_size).float()
+    row_tol = 2e-2 * want.abs().amax(dim=1, keepdim=True)
+    step0_ratio = float(((got - want).abs().amax(dim=1, keepdim=True) / row_tol).max())
+    del kref, vref
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
@@ -225,10 +416,41 @@ def stage_leg(dev, layers: int, batch: int, ctx0: int, decode_steps: int, block_
             "decode_steps": decode_steps, "block_size": block_size,
             "weight_bytes": wbytes, "mean_kv_bytes_per_step": int(kv_bytes),
             "hbm_gbs": round((wbytes + kv_bytes) / (ms * 1e-3) / 1e9, 1), "finite": finite,
+            "step0_error_over_tolerance": round(step0_ratio, 5),
+            "step0_check": ("final hidden state of step 0 against a float32 torch composition "
+                            "of the same stage (fp16 rounding at the stage's tensor "
+                            "boundaries, bit-exact dequantised weights); per row "
+                            "max|h - h_ref| / (2e-2 * ||h_ref row||_inf), <= 1 passes"),
             "workload": ("8 Llama-2-7B decoder layers (GPTQ g128 asymmetric), per layer: "
                          "RMSNorm+q/k/v (one launch), RoPE+KV-cache write (one launch), paged "
                          "attention (32 heads x 128, fp16 KV), o_proj+residual, RMSNorm, "
                          "gate/up+SiLU*mul (one launch), down+residual")}
+
+
+def host_cpu() -> dict:
+    """CPU model, physical cores (distinct (package, core) pairs) and the
+    logical CPUs this process may run on, from /proc/cpuinfo."""
+    model, cores, pkg, core = None, set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model is None:
+                    model = val
+                elif key == "physical id":
+                    pkg = val
+                elif key == "core id":
+                    core = val
+                elif not key and pkg is not None and core is not None:
+                    cores.add((pkg, core))
+                    pkg = core = None
+        if pkg is not None and core is not None:
+            cores.add((pkg, core))
+    except OSError:
+        pass
+    return {"cpu_model": model, "physical_cores": len(cores) or None,
+            "logical_cpus_allowed": len(os.sched_getaffinity(0))}
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -239,6 +461,7 @@ def cpu_baseline(seconds: float) -> dict:
     from gptq_synth import algorithmic_bytes, make_layer, make_x
     from oracle import cpu_path
 
+    # at most 16 threads: the GPU box gives one GPU's job a 16-CPU share
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     torch.set_num_threads(threads)
     lay = make_layer(4096, 4096, GROUP, seed=1000)
@@ -253,7 +476,7 @@ def cpu_baseline(seconds: float) -> dict:
     med = statistics.median(times)
     nbytes = algorithmic_bytes(1, 4096, 4096, GROUP, False)
     return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            **host_cpu(), "kind": "port",
             "sample": (f"torch-CPU dequantise+matmul (real_quant.py:69-102 restated) of one "
                        f"4096x4096 g128 asymmetric projection at M=1, {len(times)} runs, "
                        f"median {med * 1e3:.1f} ms; torch {torch.__version__}")}
@@ -355,6 +578,11 @@ def main() -> int:
     ap.add_argument("--stage-context", type=int, default=512)
     ap.add_argument("--stage-steps", type=int, default=128)
     ap.add_argument("--stage-block-size", type=int, default=16)
+    ap.add_argument("--stream-ceiling", action="store_true",
+                    help="only time the calibration streaming read in the decode launch "
+                         "shapes and exit")
+    ap.add_argument("--crossover", action="store_true",
+                    help="only time the 56-matrix pass native vs dense routes over M and exit")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -378,12 +606,18 @@ def main() -> int:
         torch.cuda.synchronize(dev)
         log(f"copied {args.copy_bytes} bytes 5 times")
         return 0
+    if args.stream_ceiling:
+        stream_ceiling(dev, args.steps)
+        return 0
     log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
     mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1))
     weight_bytes = sum(q4.qweight.numel() * 4 + q4.scales.numel() * 2 + q4.qzeros.numel() * 4
                        for _, _, _, q4 in mats)
 
     torch.cuda.synchronize(dev)
+    if args.crossover:
+        crossover(mats, dev, args.steps)
+        return 0
     if args.only_prefill:
         m = args.prefill_m
         pms, _, _ = time_graph(mats, m, args.steps, args.warmup, dev)

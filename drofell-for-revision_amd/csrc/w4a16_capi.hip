@@ -32,6 +32,21 @@ int cu_count() {
   return v;
 }
 
+}  // namespace
+
+hipError_t dw4::allow_lds(const void* kernel, size_t bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess && bit != 0) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
+
+namespace {
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_shape(int k, int n, int group_size) {
@@ -336,6 +351,34 @@ int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
   return status_of(e);
 }
 
+int dw4_dequant_bf16(int k, int n, int group_size, const int32_t* packed_qweight,
+                     const int32_t* packed_zeros, const uint16_t* packed_scales,
+                     const int32_t* perm, uint16_t* w, int64_t ldw, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (!packed_qweight || !packed_zeros || !packed_scales || !w) return DW4_ERR_INVALID_ARG;
+  if (ldw < n) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  const hipError_t e = dw4::launch_dequant_bf16(
+      reinterpret_cast<const uint32_t*>(packed_qweight),
+      reinterpret_cast<const uint32_t*>(packed_zeros), packed_scales, perm, w, ldw, k, n,
+      group_size, k / group_size, static_cast<hipStream_t>(stream));
+  return status_of(e);
+}
+
+int dw4_stream_read(const void* src, size_t bytes, int workgroups, int threads, uint32_t never,
+                    uint32_t* sink, void* stream) {
+  if (src == nullptr || sink == nullptr || workgroups <= 0 || threads <= 0) return DW4_ERR_INVALID_ARG;
+  if (threads % 64 != 0 || threads > 1024) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(src)) return DW4_ERR_MISALIGNED;
+  const size_t chunk = 1024;
+  if (bytes % ((size_t)workgroups * chunk) != 0) return DW4_ERR_INVALID_ARG;
+  const size_t per = bytes / ((size_t)workgroups * chunk);
+  if (per == 0 || per > (size_t)INT32_MAX) return DW4_ERR_INVALID_ARG;
+  return status_of(dw4::launch_stream_read(src, workgroups, threads, (int)per, never, sink,
+                                           static_cast<hipStream_t>(stream)));
+}
+
 static int check_cache_args(int num_tokens, int num_kv_heads, int head_size, int block_size,
                             const void* key, int64_t key_stride, const void* value,
                             int64_t value_stride, const int64_t* kp, const int64_t* vp,
@@ -483,6 +526,9 @@ int dw4_rope_and_cache(int num_seqs, int num_heads, int num_kv_heads, int head_d
   if (q_stride < (int64_t)num_heads * head_dim || k_stride < (int64_t)num_kv_heads * head_dim ||
       v_stride < (int64_t)num_kv_heads * head_dim || kv_head_stride < block_size * head_dim)
     return DW4_ERR_INVALID_ARG;
+  if (context_lens_out != nullptr && context_lens_out < positions + num_seqs &&
+      positions < context_lens_out + num_seqs)
+    return DW4_ERR_INVALID_ARG;  // workgroups of one sequence read positions[s] after another writes
   dw4::RopeCacheArgs a;
   a.num_seqs = num_seqs;
   a.heads = num_heads;

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 
 namespace dw4 {
 
@@ -148,6 +150,12 @@ inline bool auto_decode(int m, int n, int cus) {
   return m <= kDecodeAutoMaxM || (m <= kDecodeAutoMaxMNarrow && n / kStripN <= cus);
 }
 
+// A kernel launched with more than 64 KiB of dynamic LDS needs that size
+// allowed once per device (hipFuncSetAttribute).  `done` is the kernel's own
+// per-device record (bit d: device d allowed); concurrent first calls only
+// repeat the idempotent attribute call.
+hipError_t allow_lds(const void* kernel, size_t bytes, std::atomic<uint64_t>& done);
+
 hipError_t launch_repack(const uint32_t* qweight, const uint32_t* qzeros, const uint16_t* scales,
                          const int32_t* perm, uint32_t* pq, uint32_t* pz, uint16_t* ps,
                          int K, int N, int G, hipStream_t stream);
@@ -198,6 +206,14 @@ hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* ws,
 hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,
                           const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,
                           int G, hipStream_t stream);
+// Calibration read: `workgroups` x `threads` (a multiple of 64, at most
+// 1024), each workgroup streaming chunks_per_wg contiguous KiB of src.
+hipError_t launch_stream_read(const void* src, int workgroups, int threads, int chunks_per_wg,
+                              uint32_t never, uint32_t* sink, hipStream_t stream);
+// As launch_dequant, each value converted to bf16 (round to nearest even).
+hipError_t launch_dequant_bf16(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,
+                               const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,
+                               int G, hipStream_t stream);
 
 // Transposed product out[M, K] = g[M, N] @ W^T (PEFT backward).
 struct GemmTArgs {

@@ -1370,8 +1370,16 @@ __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M,
 
 // ---------------------------------------------------------------------------
 // Bit-exact dequantisation to the original row order (one thread per 16-byte
-// lane unit = 32 weights).
+// lane unit = 32 weights).  BF16 writes the fp16 value converted to bf16
+// (round to nearest even; a NaN stays a NaN with the quiet bit set).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint16_t bf16_of_h(_Float16 v) {
+  const uint32_t f = __builtin_bit_cast(uint32_t, (float)v);  // exact widening
+  if ((f & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((f >> 16) | 0x40u);
+  return (uint16_t)((f + 0x7fffu + ((f >> 16) & 1u)) >> 16);
+}
+
+template <bool BF16>
 __global__ void dequant_kernel(const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
                                const uint16_t* __restrict__ ps, const int32_t* __restrict__ perm,
                                uint16_t* __restrict__ w, int64_t ldw, int K, int N, int gs, int G) {
@@ -1404,9 +1412,49 @@ __global__ void dequant_kernel(const u4* __restrict__ pq, const uint32_t* __rest
       const _Float16 v = sc * (_Float16)(qv - ze);
       const int k = k0 + e;
       const int row = perm ? perm[k] : k;
-      w[(size_t)row * ldw + n] = h_bits(v);
+      w[(size_t)row * ldw + n] = BF16 ? bf16_of_h(v) : h_bits(v);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Calibration: a plain streaming read in a decode-like launch shape.
+// Workgroup b reads the contiguous byte range [b * per_wg, (b + 1) * per_wg)
+// of src; its waves take 1 KiB chunks round-robin (chunk i of the workgroup
+// goes to wave i % waves), each lane one 16-byte non-temporal load per
+// chunk, kRing chunks in flight per wave.  The words are folded into one
+// value per lane that is stored only if it equals `never` (the caller passes
+// a value the data cannot fold to), so the loads stay live without a store
+// stream.  This is the ceiling a weight-streaming kernel of the same launch
+// shape can reach.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(1024)
+stream_read_kernel(const u4* __restrict__ src, int chunks_per_wg, uint32_t never,
+                   uint32_t* __restrict__ sink) {
+  constexpr int kRing = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  const u4* base = src + (size_t)blockIdx.x * chunks_per_wg * 64 + lane;
+  u4 acc = u4{0u, 0u, 0u, 0u};
+  int c = wave;
+  for (; c + (kRing - 1) * waves < chunks_per_wg; c += kRing * waves) {
+    u4 r[kRing];
+#pragma unroll
+    for (int u = 0; u < kRing; ++u) r[u] = __builtin_nontemporal_load(base + (size_t)(c + u * waves) * 64);
+#pragma unroll
+    for (int u = 0; u < kRing; ++u) acc ^= r[u];
+  }
+  for (; c < chunks_per_wg; c += waves) acc ^= __builtin_nontemporal_load(base + (size_t)c * 64);
+  const uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  if (v == never) sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = v;
+}
+
+hipError_t launch_stream_read(const void* src, int workgroups, int threads, int chunks_per_wg,
+                              uint32_t never, uint32_t* sink, hipStream_t stream) {
+  stream_read_kernel<<<(unsigned)workgroups, (unsigned)threads, 0, stream>>>(
+      static_cast<const u4*>(src), chunks_per_wg, never, sink);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -1443,14 +1491,11 @@ static hipError_t launch_decode_one(const GemmArgs& a, const Items& d, const Dec
                                     float* part, hipStream_t stream) {
   const dim3 grid((unsigned)d.wg0[d.count], p.splits);
   if (p.smem > 64 * 1024) {
-    static bool raised = false;  // idempotent attribute; races only repeat it
-    if (!raised) {
-      const hipError_t e = hipFuncSetAttribute(
-          reinterpret_cast<const void*>(&decode_kernel<MT, WAVES, U, G128, ACT, GRP>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsPerCu);
-      if (e != hipSuccess) return e;
-      raised = true;
-    }
+    static std::atomic<uint64_t> allowed{0};
+    const hipError_t e = allow_lds(
+        reinterpret_cast<const void*>(&decode_kernel<MT, WAVES, U, G128, ACT, GRP>), kLdsPerCu,
+        allowed);
+    if (e != hipSuccess) return e;
   }
   decode_kernel<MT, WAVES, U, G128, ACT, GRP><<<grid, WAVES * 64, p.smem, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, d, part, a.K, a.gs, a.G, p.cps, div_magic(a.M),
@@ -1633,7 +1678,16 @@ hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t
                           const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs, int G,
                           hipStream_t stream) {
   const size_t total = (size_t)K * N / 32;
-  dequant_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
+  dequant_kernel<false><<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
+      (const u4*)pq, pz, ps, perm, w, ldw, K, N, gs, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant_bf16(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,
+                               const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,
+                               int G, hipStream_t stream) {
+  const size_t total = (size_t)K * N / 32;
+  dequant_kernel<true><<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(
       (const u4*)pq, pz, ps, perm, w, ldw, K, N, gs, G);
   return hipGetLastError();
 }

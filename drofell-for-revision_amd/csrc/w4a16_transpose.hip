@@ -242,14 +242,9 @@ hipError_t launch_t_cfg(const GemmTArgs& a, const GemmTPlan& p, float* part, hip
   const size_t smem = (size_t)WAVES * KBR * MT * 64 * sizeof(f4);
   auto kern = &gemm_t_kernel<MT, WAVES, t_ring<MT, GPC>(), GPC, ACT, KBR>;
   if (smem > 64 * 1024) {
-    static bool raised = false;  // idempotent attribute; races only repeat it
-    if (!raised) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)smem);
-      if (e != hipSuccess) return e;
-      raised = true;
-    }
+    static std::atomic<uint64_t> allowed{0};
+    const hipError_t e = allow_lds(reinterpret_cast<const void*>(kern), smem, allowed);
+    if (e != hipSuccess) return e;
   }
   kern<<<grid, WAVES * 64, smem, stream>>>(
       (const _Float16*)a.g, a.ldg, a.M, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps, a.perm,

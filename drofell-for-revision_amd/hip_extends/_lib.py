@@ -58,6 +58,9 @@ SIGNATURES = {
                                  _P, _c.c_size_t, _P]),
     "dw4_dequant": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
                                _c.c_int64, _P]),
+    "dw4_dequant_bf16": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
+                                    _c.c_int64, _P]),
+    "dw4_stream_read": (_c.c_int, [_P, _c.c_size_t, _c.c_int, _c.c_int, _c.c_uint32, _P, _P]),
     "dw4_gemm_t": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64, _P, _P, _P,
                               _P, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_t_workspace_size": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int,
@@ -90,7 +93,7 @@ SIGNATURES = {
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
 }
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -118,6 +118,24 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _output_rows(output: torch.Tensor, m: int, n: int, dtype: torch.dtype) -> torch.Tensor:
+    """The caller's ``output`` as a [m, n] row-major view the product can be
+    written into (unit column stride, any row stride >= n), or an error:
+    the product is never written anywhere else."""
+    if output.dtype != dtype:
+        raise TypeError(f"output is {output.dtype}, the product is {dtype}")
+    if output.device.type != "cuda":
+        raise ValueError("output must live on the device")
+    if output.numel() != m * n:
+        raise ValueError(f"output holds {output.numel()} elements, the product has {m} x {n}")
+    if output.is_contiguous():
+        return output.view(m, n)
+    if output.dim() == 2 and output.shape[0] == m and output.stride(1) == 1 \
+            and output.stride(0) >= n:
+        return output
+    raise ValueError("output must be contiguous or a [m, n] view with unit column stride")
+
+
 def _aligned_rows(x2: torch.Tensor) -> torch.Tensor:
     """A [M, K] fp16 view whose base is 16-byte aligned with ldx % 8 == 0."""
     if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
@@ -252,6 +270,7 @@ class Q4MatrixV2(object):
         cache.update_workspace_size(sizes["workspace"])
         cache.update_temp_weight_size(height * width)
         self.reconstructed_weight_float16: Optional[torch.Tensor] = None
+        self.reconstructed_weight_bfloat16: Optional[torch.Tensor] = None
 
     @property
     def cuda_q4(self) -> "Q4MatrixV2":
@@ -280,13 +299,14 @@ class Q4MatrixV2(object):
         devices = {qweight.device, qzeros.device, scales.device, perm.device}
         if len(devices) != 1:
             raise ValueError(f"packed tensors on several devices: {devices}")
-        had_dense = self.reconstructed_weight_float16 is not None
+        had = [dt for dt in (torch.float16, torch.bfloat16) if self._reconstructed(dt) is not None]
         self.qweight, self.qzeros, self.scales = qweight, qzeros, scales
         self.perm = perm
         self.device = qweight.device
-        self.reconstructed_weight_float16 = None
-        if had_dense and self.device.type == "cuda":
-            self.reconstruct_weight()
+        self.release_weight()
+        if self.device.type == "cuda":
+            for dt in had:
+                self.reconstruct_weight(dt)
 
     def _check_resident(self) -> None:
         if self.device.type != "cuda":
@@ -311,44 +331,52 @@ class Q4MatrixV2(object):
     def matmul(self, x: torch.Tensor, output: Optional[torch.Tensor] = None,
                temp_weight: Optional[torch.Tensor] = None, must_blas: bool = False, *,
                bias: Optional[torch.Tensor] = None, path: Optional[int] = None) -> torch.Tensor:
-        """``x @ W (+ bias)`` for x [..., K] in x's dtype (fp16 or bf16).
+        """``x @ W (+ bias)`` for x [..., K]; the result has x's dtype.
 
-        Same arguments as the reference (``exllama.py:492-526``): with a
-        reconstructed fp16 weight, or ``must_blas``, the product is the dense
-        one over the dequantised weight (bit-exact HIP dequantisation into
-        ``temp_weight`` or the shared buffer, then a library GEMM); otherwise
-        the HIP W4A16 kernel runs (decode kernel for small M, MFMA prefill
-        kernel above).  bf16 activations are rounded to fp16 for the
-        product.  ``bias`` (fp16 [N]) is added after the fp16 rounding of
-        the product, as ``output += bias`` does in the reference.
+        Same arguments and routes as the reference (``exllama.py:492-526``):
+
+        * fp16 x: with a reconstructed fp16 weight, or ``must_blas``, the
+          dense product over the dequantised weight (bit-exact HIP
+          dequantisation into ``temp_weight`` or the shared buffer, then a
+          library GEMM); otherwise the HIP W4A16 kernel (decode kernel for
+          small M, MFMA prefill kernel above);
+        * bf16 x: always the dense bf16 product (fp32 accumulation) over the
+          bf16 weight bf16(fp16(s * (q - z))), the reconstructed one or one
+          dequantised into ``temp_weight`` / the shared buffer, as the
+          reference's ``q4_matmul_blas_v2`` with ``bfloat16`` does.  The
+          activations keep bf16's range.
+
+        ``output`` (x's dtype, ``M * N`` elements, contiguous or a row-strided
+        [M, N] view) receives the product; anything else raises.  ``bias``
+        ([N]) is added after the rounding of the product, as the reference's
+        ``output += bias``.
         """
         self._check_resident()
         if x.device != self.device:
             raise ValueError(f"input on {x.device}, weights on {self.device}")
         if x.dtype not in (torch.float16, torch.bfloat16):
             raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
-        in_dtype = x.dtype
-        if in_dtype != torch.float16:
-            x = x.to(torch.float16)
+        dtype = x.dtype
         outshape = x.shape[:-1] + (self.width,)
-        x2 = _aligned_rows(x.reshape(-1, self.height))
-        m = x2.shape[0]
+        m = x.numel() // self.height
+        out2 = None if output is None else _output_rows(output, m, self.width, dtype)
         if bias is not None:
-            bias = bias.to(torch.float16).contiguous()
-        if must_blas or self.reconstructed_weight_float16 is not None:
-            w = self.reconstructed_weight_float16
-            if w is None:
-                w = self._dense_weight(temp_weight)
-            y = torch.matmul(x2, w)
+            bias = bias.to(dtype).contiguous()
+        dense = self._reconstructed(dtype)
+        if dense is not None or must_blas or dtype == torch.bfloat16:
+            w = dense if dense is not None else self._dense_weight(temp_weight, dtype)
+            x2 = x.reshape(m, self.height)
+            if out2 is None:
+                y = torch.matmul(x2, w)
+            else:
+                y = torch.matmul(x2, w, out=out2) if out2.is_contiguous() else \
+                    out2.copy_(torch.matmul(x2, w))
             if bias is not None:
                 y += bias
-            if output is not None:
-                output.view(m, self.width).copy_(y)
-                y = output
-            y = y.view(outshape)
-            return y if in_dtype == torch.float16 else y.to(in_dtype)
-        if output is None or output.dtype != torch.float16 or not output.is_contiguous():
-            output = torch.empty((m, self.width), dtype=torch.float16, device=self.device)
+            return y.view(outshape) if output is None else output
+        x2 = _aligned_rows(x.reshape(m, self.height))
+        if out2 is None:
+            out2 = torch.empty((m, self.width), dtype=torch.float16, device=self.device)
         ws = self.cache.workspace
         lib = _lib.load()
         status = lib.dw4_gemm_path(
@@ -357,39 +385,48 @@ class Q4MatrixV2(object):
             x2.data_ptr(), x2.stride(0),
             self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
             _ptr(self.perm) if self.use_act else None, _ptr(bias),
-            output.data_ptr(), output.stride(0) if output.dim() == 2 else self.width,
+            out2.data_ptr(), out2.stride(0),
             ws.data_ptr(), ws.numel(), _stream(self.device))
         _lib.check("dw4_gemm_path", status)
-        out = output.view(outshape)
-        return out if in_dtype == torch.float16 else out.to(in_dtype)
+        return out2.view(outshape) if output is None else output
+
+    def _reconstructed(self, dtype: torch.dtype) -> Optional[torch.Tensor]:
+        return self.reconstructed_weight_float16 if dtype == torch.float16 else \
+            self.reconstructed_weight_bfloat16
 
     def _transpose_native(self, x: torch.Tensor, output: Optional[torch.Tensor]) -> torch.Tensor:
+        """fp16 ``x @ W.T`` through the packed transposed kernel."""
         if x.device != self.device:
             raise ValueError(f"input on {x.device}, weights on {self.device}")
-        in_dtype = x.dtype
+        if x.dtype != torch.float16:
+            raise TypeError(f"the packed transposed kernel takes fp16, got {x.dtype}")
         outshape = x.shape[:-1] + (self.height,)
-        g2 = _aligned_rows(x.reshape(-1, self.width).to(torch.float16))
+        g2 = _aligned_rows(x.reshape(-1, self.width))
         m = g2.shape[0]
-        y = torch.empty((m, self.height), dtype=torch.float16, device=self.device)
+        out2 = torch.empty((m, self.height), dtype=torch.float16, device=self.device) \
+            if output is None else _output_rows(output, m, self.height, torch.float16)
         nbytes = _lib.gemm_t_workspace_size(m, self.height, self.width, self.group_size)
         ws = self.cache.transpose_workspace(nbytes)
         _lib.call("dw4_gemm_t", m, self.height, self.width, self.group_size,
                   g2.data_ptr(), g2.stride(0), self.qweight.data_ptr(), self.qzeros.data_ptr(),
                   self.scales.data_ptr(), _ptr(self.perm) if self.use_act else None,
-                  y.data_ptr(), self.height, ws.data_ptr(), ws.numel(), _stream(self.device))
-        if output is not None:
-            output.view(m, self.height).copy_(y)
-            y = output
-        y = y.view(outshape)
-        return y if in_dtype == torch.float16 else y.to(in_dtype)
+                  out2.data_ptr(), out2.stride(0), ws.data_ptr(), ws.numel(), _stream(self.device))
+        return out2.view(outshape) if output is None else output
 
-    def _dense_weight(self, temp_weight: Optional[torch.Tensor]) -> torch.Tensor:
-        """The fp16 [K, N] weight dequantised into ``temp_weight`` (or the
-        shared per-device buffer)."""
+    def _dense_weight(self, temp_weight: Optional[torch.Tensor],
+                      dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """The [K, N] weight in ``dtype`` (fp16 or bf16) dequantised into
+        ``temp_weight`` or the shared per-device buffer (fp16 storage,
+        reinterpreted for bf16 as the reference does)."""
         buf = temp_weight if temp_weight is not None else self.cache.temp_weight
-        if buf.dtype != torch.float16 or buf.numel() < self.height * self.width:
-            raise ValueError("temp_weight must be an fp16 buffer of at least K*N elements")
-        w = buf.view(-1)[: self.height * self.width].view(self.height, self.width)
+        if buf.element_size() != 2 or buf.numel() < self.height * self.width:
+            raise ValueError("temp_weight must be a 2-byte buffer of at least K*N elements")
+        flat = buf.view(-1)[: self.height * self.width]
+        if flat.dtype != dtype:
+            flat = flat.view(dtype)
+        w = flat.view(self.height, self.width)
+        if dtype == torch.bfloat16:
+            return self.get_bfloat16_weights_matrix_v2(w)
         return self.get_float16_weights_matrix_v2(w)
 
     def get_float16_weights_matrix_v2(self, out_matrix: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -406,63 +443,102 @@ class Q4MatrixV2(object):
                   w.data_ptr(), w.stride(0), _stream(self.device))
         return out_matrix
 
+    def get_bfloat16_weights_matrix_v2(self, out_matrix: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Dequantised bf16 weight [K, N] in the checkpoint's row order:
+        bf16(fp16(s * (q - z))), bit-exact with the reference's bf16
+        reconstruction (``q4_matrix.cu:469-614``)."""
+        self._check_resident()
+        if out_matrix is None:
+            out_matrix = torch.empty(self.height, self.width, dtype=torch.bfloat16,
+                                     device=self.device)
+        if out_matrix.dtype != torch.bfloat16 or \
+                tuple(out_matrix.shape[-2:]) != (self.height, self.width):
+            raise ValueError("out_matrix must be bf16 [K, N]")
+        w = out_matrix.view(self.height, self.width)
+        _lib.call("dw4_dequant_bf16", self.height, self.width, self.group_size,
+                  self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
+                  _ptr(self.perm) if self.use_act else None,
+                  w.data_ptr(), w.stride(0), _stream(self.device))
+        return out_matrix
+
     def reconstruct_weight(self, dtype: torch.dtype = torch.float16) -> None:
-        if dtype != torch.float16:
-            raise ValueError("only fp16 reconstruction is supported")
-        self.reconstructed_weight_float16 = self.get_float16_weights_matrix_v2()
+        if dtype == torch.float16:
+            self.reconstructed_weight_float16 = self.get_float16_weights_matrix_v2()
+        elif dtype == torch.bfloat16:
+            self.reconstructed_weight_bfloat16 = self.get_bfloat16_weights_matrix_v2()
+        else:
+            raise ValueError(f"reconstruction dtype must be fp16 or bf16, got {dtype}")
 
     def release_weight(self, dtype: Optional[torch.dtype] = None) -> None:
-        self.reconstructed_weight_float16 = None
+        if dtype in (None, torch.float16):
+            self.reconstructed_weight_float16 = None
+        if dtype in (None, torch.bfloat16):
+            self.reconstructed_weight_bfloat16 = None
 
     def transpose_matmul(self, x: torch.Tensor, output: Optional[torch.Tensor] = None,
                          temp_weight: Optional[torch.Tensor] = None,
                          skip_reconstruct: bool = False) -> torch.Tensor:
-        """``x @ W.T`` for x [..., N] (the activation gradient of the forward).
+        """``x @ W.T`` for x [..., N] (the activation gradient of the forward),
+        in x's dtype.
 
         Same arguments as the reference (``exllama.py:528-544``).  With a
-        reconstructed weight, or ``skip_reconstruct`` (the caller already
-        filled ``temp_weight``), the product is the dense one over that
-        weight.  Otherwise, up to ``TuningParams.TRANSPOSE_MAX_M`` rows, the
-        packed kernel (``dw4_gemm_t``) reads the int4 words directly; above
-        it the weight is dequantised bit-exactly into ``temp_weight`` (or the
-        shared buffer) and a library GEMM runs, as in the reference.
+        reconstructed weight of x's dtype, or ``skip_reconstruct`` (the caller
+        already filled ``temp_weight``), the product is the dense one over
+        that weight.  Otherwise fp16 x up to ``TuningParams.TRANSPOSE_MAX_M``
+        rows runs the packed kernel (``dw4_gemm_t``), which reads the int4
+        words directly; above it, and for bf16 x, the weight is dequantised
+        bit-exactly (fp16, or bf16 of the fp16 value) into ``temp_weight`` or
+        the shared buffer and a library GEMM runs, as in the reference.
         """
         if x.dtype not in (torch.float16, torch.bfloat16):
             raise TypeError(f"activations must be fp16 or bf16, got {x.dtype}")
         self._check_resident()
+        dtype = x.dtype
         m = x.numel() // self.width
-        if self.reconstructed_weight_float16 is None and not skip_reconstruct \
+        w = self._reconstructed(dtype)
+        if w is None and not skip_reconstruct and dtype == torch.float16 \
                 and 0 < m <= self.tuning_params.TRANSPOSE_MAX_M:
             return self._transpose_native(x, output)
-        w = self.reconstructed_weight_float16
         if w is None:
             if skip_reconstruct:
                 if temp_weight is None:
                     raise ValueError("skip_reconstruct needs the filled temp_weight")
+                if temp_weight.dtype != dtype:
+                    raise TypeError(f"temp_weight is {temp_weight.dtype}, x is {dtype}")
                 w = temp_weight.view(-1)[: self.height * self.width].view(self.height, self.width)
             else:
-                w = self._dense_weight(temp_weight)
-        in_dtype = x.dtype
+                w = self._dense_weight(temp_weight, dtype)
         outshape = x.shape[:-1] + (self.height,)
-        y = torch.matmul(x.reshape(-1, self.width).to(torch.float16), w.t())
-        if output is not None:
-            output.view(-1, self.height).copy_(y)
-            y = output
-        y = y.view(outshape)
-        return y if in_dtype == torch.float16 else y.to(in_dtype)
+        y = torch.matmul(x.reshape(m, self.width), w.t())
+        if output is None:
+            return y.view(outshape)
+        _output_rows(output, m, self.height, dtype).copy_(y)
+        return output
 
 
 class Q4LinearFunction(Function):
-    """Frozen quantised weight; only the activation receives a gradient."""
+    """Frozen quantised weight; only the activation receives a gradient.
+
+    As ``ExllamaQ4LinearFunction`` (``exllama.py:649-696``): with
+    ``cache_weight`` the dequantised weight of the input's dtype is kept for
+    the backward (unless the matrix already holds a reconstructed one);
+    the forward of fp16 input still runs the W4A16 kernel, bf16 input the
+    dense product over the kept weight.
+    """
 
     @staticmethod
     def forward(ctx: Any, input: torch.Tensor, weight_q4: Q4MatrixV2,  # type: ignore[override]
                 bias: Optional[torch.Tensor], cache_weight: bool) -> torch.Tensor:
         ctx.weight_q4 = weight_q4
         cached = None
-        if cache_weight and weight_q4.reconstructed_weight_float16 is None:
-            cached = weight_q4.get_float16_weights_matrix_v2()
-        output = weight_q4.matmul(input, bias=bias)
+        if cache_weight and weight_q4._reconstructed(input.dtype) is None:
+            cached = weight_q4._dense_weight(
+                torch.empty(weight_q4.height * weight_q4.width, dtype=input.dtype,
+                            device=weight_q4.device), input.dtype)
+        if cached is not None and input.dtype == torch.bfloat16:
+            output = weight_q4.matmul(input, temp_weight=cached, must_blas=True, bias=bias)
+        else:
+            output = weight_q4.matmul(input, bias=bias)
         if cached is not None:
             ctx.save_for_backward(cached)
         ctx.has_cached = cached is not None
@@ -576,20 +652,36 @@ def attention_forward_rope_stage_v2_py(temp_q_output: torch.Tensor, temp_k_outpu
     """Rotary embedding of q and k in place (``exllama.py:133-135`` ->
     ``fuse_v2/rope.cu``): row r of batch entry b takes position
     ``(past_len if past_len >= 0 else past_lens[b]) + r // heads`` of the fp16
-    tables ``sin`` / ``cos`` [max_positions, head_dim]."""
+    tables ``sin`` / ``cos``, each [..., max_positions, head_dim] (the
+    reference's rotary modules keep them as [1, 1, max_positions, head_dim],
+    ``operators/core/rope/real.py:114,140``)."""
     lens = None
     if past_len < 0:
         if past_lens is None:
             raise ValueError("past_len -1 needs past_lens")
         lens = past_lens.to(device=temp_q_output.device, dtype=torch.int32).contiguous()
-    s16 = sin.to(torch.float16).contiguous()
-    c16 = cos.to(torch.float16).contiguous()
+    s16, c16, max_pos = rope_tables(sin, cos, head_dim)
     for t, heads in ((temp_q_output, num_heads), (temp_k_output, num_kv_heads)):
         if t.dtype != torch.float16 or not t.is_contiguous():
             raise TypeError("q/k must be contiguous fp16")
         _lib.call("dw4_rope", batch_size, q_len * heads, heads, head_dim, t.data_ptr(),
-                  s16.data_ptr(), c16.data_ptr(), s16.shape[0], past_len,
+                  s16.data_ptr(), c16.data_ptr(), max_pos, past_len,
                   None if lens is None else lens.data_ptr(), _stream(t.device))
+
+
+def rope_tables(sin: torch.Tensor, cos: torch.Tensor,
+                head_dim: int) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    """fp16 sin / cos tables as contiguous [positions, head_dim] and the
+    position count, from tables of any leading shape ending in head_dim
+    ([P, hd] or the rotary modules' [1, 1, P, hd])."""
+    if sin.shape != cos.shape:
+        raise ValueError(f"sin {tuple(sin.shape)} and cos {tuple(cos.shape)} differ")
+    if sin.dim() < 1 or sin.shape[-1] != head_dim:
+        raise ValueError(f"rope tables end in {sin.shape[-1] if sin.dim() else None}, "
+                         f"head_dim is {head_dim}")
+    s16 = sin.to(torch.float16).contiguous().view(-1, head_dim)
+    c16 = cos.to(torch.float16).contiguous().view(-1, head_dim)
+    return s16, c16, s16.shape[0]
 
 
 def mlp_forward_v2_py(layernorm: torch.Tensor, norm_epsilon: float, gate_q4: Any, up_q4: Any,

@@ -15,6 +15,7 @@ from typing import List, Optional, Tuple
 import torch
 
 from hip_extends import _lib
+from hip_extends.w4a16 import rope_tables
 
 from ... import flags
 from .common import BlockInfo
@@ -22,6 +23,11 @@ from .common import BlockInfo
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
 
 
 class LayerBlocksHolder:
@@ -106,17 +112,21 @@ class LayerBlocksHolder:
         if k.shape != v.shape or k.shape[0] != seqs or hd != self.block_info.head_dim or \
                 kvh != self.block_info.num_key_value_heads:
             raise AssertionError("q/k/v shapes do not match the block geometry")
-        for t in (q, k, v, sin, cos):
+        for t in (q, k, v):
             if t.dtype != torch.float16 or not t.is_contiguous():
-                raise TypeError("q, k, v, sin, cos must be contiguous fp16")
+                raise TypeError("q, k, v must be contiguous fp16")
+        s16, c16, max_pos = rope_tables(sin, cos, hd)
         if context_lens_out is not None and (context_lens_out.dtype != torch.int32 or
                                              context_lens_out.numel() < seqs):
             raise TypeError("context_lens_out must be int32 with one entry per sequence")
         pos = positions.to(torch.int32).contiguous()
+        if context_lens_out is not None and _overlaps(pos, context_lens_out):
+            raise ValueError("context_lens_out must not share memory with positions: the "
+                             "launch reads every position after writing the first lengths")
         tables = block_tables.to(torch.int32).contiguous()
         _lib.call("dw4_rope_and_cache", seqs, heads, kvh, hd, flags.BLOCK_SIZE, q.data_ptr(),
                   q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0),
-                  sin.data_ptr(), cos.data_ptr(), sin.shape[0], pos.data_ptr(), tables.data_ptr(),
+                  s16.data_ptr(), c16.data_ptr(), max_pos, pos.data_ptr(), tables.data_ptr(),
                   tables.shape[1], self.layer_key_ptr_table_device.data_ptr(),
                   self.layer_val_ptr_table_device.data_ptr(), self.block_info.head_stride,
                   None if context_lens_out is None else context_lens_out.data_ptr(),

@@ -124,6 +124,9 @@ class QuantLinearMemoryModel(MemoryModule):
         if flags.RECONSTRUCTE_WEIGTH_FLOAT16:
             self.reconstructed_weight = MemoryTensor((self.infeatures, self.outfeatures),
                                                      torch.float16)
+        if flags.RECONSTRUCTE_WEIGTH_BFLOAT16:
+            self.reconstructed_weight_bfloat16 = MemoryTensor(
+                (self.infeatures, self.outfeatures), torch.bfloat16)
         cache.update_workspace_size(_workspace_bytes(
             self.infeatures, self.outfeatures, self.group_size, self.use_act_order,
             tunning_params.MAX_M))

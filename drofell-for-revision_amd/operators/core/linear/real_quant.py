@@ -90,7 +90,7 @@ class QuantLinear(Linear):
         if flags.RECONSTRUCTE_WEIGTH_FLOAT16:
             q4.reconstruct_weight(dtype=torch.float16)
         if flags.RECONSTRUCTE_WEIGTH_BFLOAT16:
-            raise RuntimeError("bf16 reconstruction is not supported by the HIP backend")
+            q4.reconstruct_weight(dtype=torch.bfloat16)
 
     def _apply(self, fn, recurse: bool = True):
         """Module moves (swap-out to host memory, swap-in to a device) carry

@@ -46,7 +46,9 @@
  *     abort crosses the ABI.  dw4_strerror() names a status.
  *   - Every buffer is owned by the caller.  The library allocates nothing
  *     on the device, keeps no pointer after a call returns and holds no
- *     global mutable state except a per-device property cache.
+ *     global mutable state except per-device records: the CU count and,
+ *     per kernel, whether its dynamic LDS limit has been raised on that
+ *     device.
  *   - Device pointers refer to memory of the current HIP device; `stream`
  *     is a hipStream_t (NULL = the null stream).  Work is enqueued on it.
  *   - dw4_gemm never synchronises, never allocates and launches a fixed
@@ -97,7 +99,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 7
+#define DW4_ABI_VERSION 8
 
 enum {
   DW4_OK = 0,
@@ -173,6 +175,29 @@ int dw4_dequant(int k, int n, int group_size,
                 const int32_t* packed_qweight, const int32_t* packed_zeros,
                 const uint16_t* packed_scales, const int32_t* perm,
                 uint16_t* w, int64_t ldw, void* stream);
+
+/* Device: the bf16 weight w[K, N] (row stride ldw) in ORIGINAL row order,
+ * bit-exact with bf16_rne(fp16_rne(scale * (q - (zero + 1)))): the fp16
+ * dequantised value converted to bf16, as the reference's bf16 route
+ * computes it.  Replaces reconstruct_nv_bfloat16_exllama_v2
+ * (cuda_extends/exllama/q4_matrix.cu:469-614), which q4_matmul_blas_v2
+ * (entry.cpp:303-340 -> q4_matmul.cu:459-494) runs before its bf16 GEMM. */
+int dw4_dequant_bf16(int k, int n, int group_size,
+                     const int32_t* packed_qweight, const int32_t* packed_zeros,
+                     const uint16_t* packed_scales, const int32_t* perm,
+                     uint16_t* w, int64_t ldw, void* stream);
+
+/* Calibration (no reference counterpart): a plain streaming read of `bytes`
+ * of device memory at src in a decode-like launch shape -- `workgroups`
+ * workgroups of `threads` threads (a multiple of 64, at most 1024), each
+ * reading its contiguous bytes / workgroups range in 1 KiB wave loads of
+ * 16 bytes per lane, four per wave in flight.  bytes must be a multiple of
+ * workgroups * 1024.  Nothing is written unless the folded words equal
+ * `never`; then sink (workgroups * threads uint32) receives them.  The
+ * benchmark times it to state the HBM ceiling a weight-streaming launch of
+ * that shape can reach. */
+int dw4_stream_read(const void* src, size_t bytes, int workgroups, int threads, uint32_t never,
+                    uint32_t* sink, void* stream);
 
 /* out = g @ W^T, the activation gradient of y = x @ W (PEFT backward):
  * g fp16 [m, n] (row stride ldg), out fp16 [m, k] (row stride ldo) in the
@@ -347,8 +372,10 @@ int dw4_rope(int batch_size, int rows_per_batch, int num_heads, int head_dim, ui
  * decode loop) in one launch.  q [num_seqs][num_heads][head_dim],
  * k, v [num_seqs][num_kv_heads][head_dim] fp16 with per-sequence strides.
  * A position outside the block table writes no slot; one outside the
- * sin/cos tables leaves the rows unrotated.  No counterpart in the
- * reference as a single call. */
+ * sin/cos tables leaves the rows unrotated.  context_lens_out must not
+ * overlap positions (an in-place advance would race with the workgroups of
+ * the same sequence that still read the position): DW4_ERR_INVALID_ARG.
+ * No counterpart in the reference as a single call. */
 int dw4_rope_and_cache(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
                        int block_size, uint16_t* q, int64_t q_stride, uint16_t* k,
                        int64_t k_stride, const uint16_t* v, int64_t v_stride,

@@ -25,7 +25,9 @@ It restates, in numpy, the arithmetic the reference defines for one GPTQ
 * the act-order row order (stable counting sort of rows by ``g_idx``,
   ``x_map[new] = old``) -- ``q4_matrix.cu:125-159`` (``make_sequential``);
 * the forward ``y = x @ W`` (+ optional fp16 bias) --
-  ``cuda_extends/exllama.py:492-526,730-736``.
+  ``cuda_extends/exllama.py:492-526,730-736``;
+* the bf16 route's weight ``bf16(W)`` (fp16 value rounded to bfloat16) --
+  ``q4_matrix.cu:465-467,583-601``, ``q4_matmul.cu:480-494``.
 
 Parity status of every function here is pinned by ``tests/test_oracle.py``
 (closed forms, an exhaustive dequant known-answer table against an
@@ -110,6 +112,34 @@ def dequantize(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray,
     d = (q - z[gi]).astype(np.float32)
     s = np.asarray(scales, dtype=np.float16)[gi].astype(np.float32)
     return (s * d).astype(np.float16)
+
+
+def bf16_bits(w: np.ndarray) -> np.ndarray:
+    """uint16 bfloat16 bit patterns of fp16 values: each (exact) value
+    rounded once to bfloat16, to nearest, ties to even.
+
+    The reference's bf16 route converts the fp16 dequantised value with
+    ``__float2bfloat16(__half2float(v))`` (``q4_matrix.cu:465-467``, used at
+    ``:583-601`` by ``reconstruct_gptq_kernel_nv_bfloat16``).  A NaN maps to
+    a quiet NaN of the same sign (checks compare NaNs as a class).
+    """
+    f = np.asarray(w, dtype=np.float16).astype(np.float32).view(np.uint32).astype(np.uint64)
+    nan = (f & 0x7FFFFFFF) > 0x7F800000
+    rne = (f + 0x7FFF + ((f >> 16) & 1)) >> 16
+    return np.where(nan, (f >> 16) | 0x40, rne).astype(np.uint16)
+
+
+def bf16_to_float(bits: np.ndarray) -> np.ndarray:
+    """float32 values of uint16 bfloat16 bit patterns (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def dequantize_bf16(qweight: np.ndarray, qzeros: np.ndarray, scales: np.ndarray,
+                    g_idx: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bit patterns [K, N] of the weight the reference's bf16 route
+    multiplies by: bf16_rne(fp16 dequantised weight), ORIGINAL row order
+    (``q4_matrix.cu:469-614``)."""
+    return bf16_bits(dequantize(qweight, qzeros, scales, g_idx))
 
 
 def act_order_perm(g_idx: np.ndarray, groups: int) -> np.ndarray:

@@ -197,8 +197,11 @@ def test_attention_statuses(hip_device):
                                      None) == _lib.DW4_ERR_UNSUPPORTED  # head size % 8
 
 
+@pytest.mark.parametrize("table_dims", [2, 4], ids=["P_hd", "1_1_P_hd"])
 @pytest.mark.parametrize("past", [3, -1])
-def test_rope_bit_exact(hip_device, past):
+def test_rope_bit_exact(hip_device, past, table_dims):
+    """Tables as [P, hd] and as the rotary modules' [1, 1, P, hd]
+    (operators/core/rope/real.py:114,140 in the reference)."""
     from hip_extends.w4a16 import attention_forward_rope_stage_v2_py
     rng = np.random.default_rng(21)
     batch, q_len, heads, kvh, hd = 3, 2, 4, 2, 128
@@ -206,11 +209,13 @@ def test_rope_bit_exact(hip_device, past):
     q = (rng.standard_normal((batch, q_len * heads, hd)) * 3).astype(np.float16)
     k = (rng.standard_normal((batch, q_len * kvh, hd)) * 3).astype(np.float16)
     lens = np.array([0, 17, 39], np.int32)  # the last one runs past the table (row left as is)
-    say(f"rope past={past}")
+    say(f"rope past={past} tables {table_dims}-d")
     qd, kd = torch.from_numpy(q).to(hip_device), torch.from_numpy(k).to(hip_device)
-    attention_forward_rope_stage_v2_py(qd, kd, torch.from_numpy(sin).to(hip_device),
-                                       torch.from_numpy(cos).to(hip_device), q_len, batch, heads,
-                                       kvh, hd, past, torch.from_numpy(lens).to(hip_device))
+    shape = sin.shape if table_dims == 2 else (1, 1) + sin.shape
+    attention_forward_rope_stage_v2_py(qd, kd, torch.from_numpy(sin).view(shape).to(hip_device),
+                                       torch.from_numpy(cos).view(shape).to(hip_device), q_len,
+                                       batch, heads, kvh, hd, past,
+                                       torch.from_numpy(lens).to(hip_device))
     torch.cuda.synchronize()
     qr = A.rope(q, sin, cos, heads, past, lens)
     kr = A.rope(k, sin, cos, kvh, past, lens)
@@ -238,9 +243,10 @@ def test_rope_and_cache_bit_exact(hip_device):
     tables = rng.permutation(nblocks)[:seqs * mb].reshape(seqs, mb).astype(np.int32)
     lens = torch.full((seqs,), -7, dtype=torch.int32, device=hip_device)
     qd, kd, vd = (torch.from_numpy(a).to(hip_device) for a in (q, k, v))
-    say("rope_and_cache")
-    holder.rope_and_cache(qd, kd, vd, torch.from_numpy(sin).to(hip_device),
-                          torch.from_numpy(cos).to(hip_device), torch.from_numpy(pos).to(hip_device),
+    say("rope_and_cache (tables [1, 1, P, hd])")
+    holder.rope_and_cache(qd, kd, vd, torch.from_numpy(sin)[None, None].to(hip_device),
+                          torch.from_numpy(cos)[None, None].to(hip_device),
+                          torch.from_numpy(pos).to(hip_device),
                           torch.from_numpy(tables).to(hip_device), lens)
     torch.cuda.synchronize()
     q_ref = A.rope(q.reshape(seqs, 1 * heads, hd), sin, cos, heads, -1, pos).reshape(q.shape)
@@ -254,3 +260,17 @@ def test_rope_and_cache_bit_exact(hip_device):
     assert np.array_equal(kt.cpu().numpy().view(np.uint16), kc.view(np.uint16))
     assert np.array_equal(vt.cpu().numpy().view(np.uint16), vc.view(np.uint16))
     assert lens.cpu().tolist() == (pos + 1).tolist()
+    say("rope_and_cache rejects context_lens_out aliasing positions")
+    posd = torch.from_numpy(pos).to(hip_device)
+    with pytest.raises(ValueError):
+        holder.rope_and_cache(qd, kd, vd, torch.from_numpy(sin).to(hip_device),
+                              torch.from_numpy(cos).to(hip_device), posd,
+                              torch.from_numpy(tables).to(hip_device), posd)
+    st = _lib.load().dw4_rope_and_cache(
+        seqs, heads, kvh, hd, bs, qd.data_ptr(), heads * hd, kd.data_ptr(), kvh * hd,
+        vd.data_ptr(), kvh * hd, torch.from_numpy(sin).to(hip_device).data_ptr(),
+        torch.from_numpy(cos).to(hip_device).data_ptr(), sin.shape[0], posd.data_ptr(),
+        torch.from_numpy(tables).to(hip_device).data_ptr(), mb,
+        holder.layer_key_ptr_table_device.data_ptr(), holder.layer_val_ptr_table_device.data_ptr(),
+        info.head_stride, posd.data_ptr() + 4, None)
+    assert st == _lib.DW4_ERR_INVALID_ARG

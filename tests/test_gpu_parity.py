@@ -270,6 +270,39 @@ def test_prefill_large_m_and_split_k(hip_device):
         check_tol(y, ref, f"M=2048 split {split}")
 
 
+@pytest.mark.parametrize("kn", SHAPES_7B, ids=lambda kn: f"{kn[0]}x{kn[1]}")
+def test_prefill_7b_large_m(hip_device, kn):
+    """Config 3 at M = 1024 and 2048 on every 7B shape through the automatic
+    path (128-row tiles above M = 512)."""
+    k, n = kn
+    lay, w = oracle_w(k, n, 128, 1000 + SHAPES_7B.index(kn), False, False)
+    q4 = build(lay, hip_device)
+    for m in (1024, 2048):
+        say(f"prefill 7B {k}x{n} M={m}")
+        x = make_x(m, k, seed=m + 13)
+        y = q4.matmul(x.to(hip_device))
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"prefill {k}x{n} M={m}")
+
+
+@pytest.mark.parametrize("k,n,m,g,act", [(1024, 400, 600, 128, False), (2048, 4112, 1000, 128, False),
+                                         (1024, 400, 700, 64, True), (1024, 272, 520, 32, True)],
+                         ids=["1024x400_M600", "2048x4112_M1000", "1024x400_M700_g64_act",
+                              "1024x272_M520_g32_act"])
+def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
+    """128-row tiles (M > 512) with a partial last row tile and a partial
+    last column tile (N not a multiple of the 128/256-column tile)."""
+    lay, w = oracle_w(k, n, g, 5000 + m, False, act)
+    q4 = build(lay, hip_device)
+    for split in (0, 1, 2):
+        say(f"prefill 128-row tiles {k}x{n} M={m} g={g} act={act} split={split}")
+        q4.tuning_params = TuningParams(PREFILL_SPLIT_K=split)
+        x = make_x(m, k, seed=m + g)
+        y = q4.matmul(x.to(hip_device), path=_lib.DW4_PATH_PREFILL)
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"{k}x{n} M={m} split {split}")
+
+
 def test_shared_workspace_across_shapes(hip_device):
     """Two matrices share one workspace; decode split-K partials and prefill
     split-K calls of different tile counts alternate on it.  Each result
@@ -330,8 +363,9 @@ def test_operator_routes(hip_device):
     yb = lin(xd.to(torch.bfloat16))
     torch.cuda.synchronize()
     assert yb.dtype == torch.bfloat16
-    check_tol(yb.float(), gptq.gemm_ref(x.to(torch.bfloat16).half().numpy(), w)
-              + bias.float().numpy(), "bf16 forward")
+    wb = gptq.bf16_to_float(gptq.bf16_bits(w)).astype(np.float64)
+    check_tol(yb.float(), x.to(torch.bfloat16).double().numpy() @ wb
+              + bias.to(torch.bfloat16).double().numpy(), "bf16 forward")
     say("operator: must_blas dense route")
     yd = q4.matmul(xd, None, None, True, bias=bias.to(hip_device))
     torch.cuda.synchronize()
@@ -449,3 +483,100 @@ def test_errors_surface(hip_device):
     ref = q4.matmul(xv.contiguous())
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+# ---------------------------------------------------------------------------
+# bf16 route (dequantise to bf16, dense bf16 product with fp32 accumulation)
+# ---------------------------------------------------------------------------
+def test_bf16_dequant_exhaustive_kat(hip_device):
+    """bf16 weights: all 16 q x 16 stored zeros x 65,536 fp16 scale patterns,
+    bit for bit against bf16(oracle fp16 weight) (NaNs as a class)."""
+    say("exhaustive bf16 dequant KAT K=512 N=65536 g=32")
+    K, N, G = 512, 65536, 16
+    q = np.zeros((K, N), dtype=np.uint8)
+    for z in range(16):
+        for qq in range(16):
+            q[z * 32 + 2 * qq: z * 32 + 2 * qq + 2, :] = qq
+    zeros = np.repeat(np.arange(16, dtype=np.uint8)[:, None], N, axis=1)
+    srow = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    scales = np.repeat(srow[None, :], G, axis=0).view(np.float16)
+    qweight, qzeros = gptq.pack_qweight(q), gptq.pack_qzeros(zeros)
+    g_idx = (np.arange(K) // 32).astype(np.int32)
+    with np.errstate(all="ignore"):
+        ref = gptq.dequantize_bf16(qweight, qzeros, scales, g_idx)
+    cache = CacheV2(hip_device)
+    q4 = Q4MatrixV2(torch.from_numpy(qweight).to(hip_device), torch.from_numpy(qzeros).to(hip_device),
+                    torch.from_numpy(scales).to(hip_device), K, N, None, False, TuningParams(), cache)
+    w = q4.get_bfloat16_weights_matrix_v2().view(torch.int16).cpu().numpy().view(np.uint16)
+    nan = np.isnan(gptq.bf16_to_float(ref))
+    same = (w == ref) | (nan & np.isnan(gptq.bf16_to_float(w)))
+    assert same.all(), np.argwhere(~same)[:5]
+
+
+@pytest.mark.parametrize("act", [False, True], ids=["plain", "act"])
+def test_bf16_route_beyond_fp16_range(hip_device, act):
+    """bf16 activations whose values exceed fp16's range (|x| up to 3e5):
+    the product keeps them (fp16 narrowing would give inf), within the
+    GEMM tolerance of the float64 product of x and the bf16 oracle weight;
+    the activation gradient takes the same bf16 route."""
+    k, n = 1024, 768
+    lay, _ = oracle_w(k, n, 128, 515 + act, False, act)
+    a = lay.numpy()
+    wb = gptq.bf16_to_float(gptq.dequantize_bf16(a["qweight"], a["qzeros"], a["scales"],
+                                                 a["g_idx"])).astype(np.float64)
+    q4 = build(lay, hip_device)
+    gen = torch.Generator().manual_seed(31)
+    for m in (1, 16, 300):
+        say(f"bf16 route act={act} M={m}")
+        x = (torch.randn(m, k, generator=gen) * 1e5).to(torch.bfloat16)
+        assert float(x.float().abs().max()) > 65504.0
+        xd = x.to(hip_device)
+        y = q4.matmul(xd)
+        torch.cuda.synchronize()
+        assert y.dtype == torch.bfloat16
+        ref = x.double().numpy() @ wb
+        check_tol(y.float(), ref, f"bf16 forward M={m}")
+        g = (torch.randn(m, n, generator=gen) * 1e5).to(torch.bfloat16)
+        gx = q4.transpose_matmul(g.to(hip_device))
+        torch.cuda.synchronize()
+        assert gx.dtype == torch.bfloat16
+        check_tol(gx.float(), g.double().numpy() @ wb.T, f"bf16 transpose M={m}")
+    say("bf16 reconstructed-weight route")
+    q4.reconstruct_weight(torch.bfloat16)
+    assert torch.equal(q4.reconstructed_weight_bfloat16.view(torch.int16).cpu(),
+                       torch.from_numpy(gptq.dequantize_bf16(
+                           a["qweight"], a["qzeros"], a["scales"], a["g_idx"]).view(np.int16)))
+    x = (torch.randn(8, k, generator=gen) * 1e5).to(torch.bfloat16)
+    y = q4.matmul(x.to(hip_device))
+    q4.release_weight(torch.bfloat16)
+    torch.cuda.synchronize()
+    check_tol(y.float(), x.double().numpy() @ wb, "bf16 reconstructed")
+
+
+def test_output_argument_contract(hip_device):
+    """A caller's output receives the product or the call raises: row-strided
+    [M, N] views are written in place; wrong dtype, wrong size or a
+    non-row-major layout raise before any launch."""
+    lay, w = oracle_w(4096, 4096, 128, 1000, False, False)
+    q4 = build(lay, hip_device)
+    for m, path in ((4, _lib.DW4_PATH_DECODE), (96, _lib.DW4_PATH_PREFILL)):
+        say(f"output contract M={m} path={path}")
+        x = make_x(m, 4096, seed=m + 900).to(hip_device)
+        ref = q4.matmul(x, path=path)
+        big = torch.full((m, 4096 + 64), -7.0, dtype=torch.float16, device=hip_device)
+        view = big[:, 32:32 + 4096]
+        got = q4.matmul(x, output=view, path=path)
+        torch.cuda.synchronize()
+        assert got is view
+        assert torch.equal(view, ref)
+        assert bool((big[:, :32] == -7.0).all()) and bool((big[:, 32 + 4096:] == -7.0).all())
+        flat = torch.empty(m * 4096, dtype=torch.float16, device=hip_device)
+        got = q4.matmul(x, output=flat, path=path)
+        torch.cuda.synchronize()
+        assert got is flat and torch.equal(flat.view(m, 4096), ref)
+        with pytest.raises(TypeError):
+            q4.matmul(x, output=torch.empty(m, 4096, dtype=torch.float32, device=hip_device))
+        with pytest.raises(ValueError):
+            q4.matmul(x, output=torch.empty(m, 4095, dtype=torch.float16, device=hip_device))
+        with pytest.raises(ValueError):
+            q4.matmul(x, output=torch.empty(4096, m, dtype=torch.float16, device=hip_device).t())

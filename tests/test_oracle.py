@@ -590,3 +590,88 @@ def test_after_stage_checks_catch_planted_mistakes(name):
         base = res if name == "out_from_residual" else x2
         return x2, rms, h, stage.add_fp16(base, d.astype(np.float16))
     assert _after_stage_checks(mutant) != []
+
+
+# ---------------------------------------------------------------------------
+# bf16 route: bf16 of the fp16 dequantised weight
+# ---------------------------------------------------------------------------
+ALL_FP16 = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+
+
+def _bf16_exact(v: float) -> int:
+    """bf16 pattern of a finite float by exact rational round-to-nearest-even
+    (8 significant bits, exponent range of float32; inputs here are fp16
+    values, far inside it)."""
+    if v == 0.0:
+        return 0x8000 if np.signbit(v) else 0
+    if np.isinf(v):
+        return 0xFF80 if v < 0 else 0x7F80
+    a = Fraction(abs(v))
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    q = Fraction(2) ** (e - 7)  # spacing of bf16 values in [2^e, 2^(e+1))
+    n = a / q
+    m = n.numerator // n.denominator
+    rem = n - m
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and m % 2 == 1):
+        m += 1
+    if m == 256:  # carried into the next binade
+        m, e = 128, e + 1
+    bits = ((e + 127) << 7) | (m - 128)
+    return bits | (0x8000 if v < 0 else 0)
+
+
+def test_bf16_bits_match_library_conversion_on_every_fp16():
+    """Every one of the 65,536 fp16 patterns against torch's float -> bf16
+    conversion (round to nearest even); NaNs stay NaNs."""
+    import torch
+    ours = gptq.bf16_bits(ALL_FP16)
+    lib = torch.from_numpy(ALL_FP16.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(ALL_FP16)
+    assert np.array_equal(ours[~nan], lib[~nan])
+    assert np.all(np.isnan(gptq.bf16_to_float(ours[nan])))
+
+
+def test_bf16_bits_match_exact_rounding():
+    """A spread of fp16 values (every 61st pattern, plus ties and the
+    extremes) against exact rational round-to-nearest-even."""
+    pats = np.concatenate([np.arange(0, 65536, 61), [0x0001, 0x03FF, 0x7BFF, 0xFBFF, 0x3C01,
+                                                     0x3C02, 0x3C03, 0x3C04, 0x3C05, 0x3C06,
+                                                     0x7C00, 0xFC00, 0x8000]]).astype(np.uint16)
+    vals = pats.view(np.float16)
+    vals = vals[~np.isnan(vals)]
+    ours = gptq.bf16_bits(vals)
+    want = np.array([_bf16_exact(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(ours, want)
+
+
+def test_bf16_ties_go_to_even():
+    """fp16 1 + k*2^-10 sits exactly halfway between bf16 neighbours for
+    odd multiples of 2^-8 / 2: 1+2^-8 -> 1 (even), 1+3*2^-8 -> 1+2^-6 (even)."""
+    one = np.float16(1.0)
+    assert gptq.bf16_bits(np.float16(one + np.float16(2.0 ** -8)))[()] == 0x3F80
+    assert gptq.bf16_bits(np.float16(one + np.float16(3 * 2.0 ** -8)))[()] == 0x3F82
+
+
+@pytest.mark.parametrize("mutant", ["truncate", "round_half_up"])
+def test_bf16_checks_catch_planted_mistakes(mutant):
+    f = ALL_FP16[~np.isnan(ALL_FP16)].astype(np.float32).view(np.uint32).astype(np.uint64)
+    if mutant == "truncate":
+        bad = (f >> 16).astype(np.uint16)
+    else:
+        bad = ((f + 0x8000) >> 16).astype(np.uint16)
+    ours = gptq.bf16_bits(ALL_FP16[~np.isnan(ALL_FP16)])
+    assert not np.array_equal(bad, ours)
+
+
+def test_dequantize_bf16_is_bf16_of_fp16_weight():
+    lay_q = np.random.default_rng(3).integers(0, 16, (256, 64)).astype(np.uint8)
+    qweight = gptq.pack_qweight(lay_q)
+    qzeros = gptq.pack_qzeros(np.random.default_rng(4).integers(0, 16, (2, 64)).astype(np.uint8))
+    scales = (np.abs(np.random.default_rng(5).standard_normal((2, 64))) * 3 + 1e-3).astype(np.float16)
+    g = gptq.default_g_idx(256, 128)
+    w = gptq.dequantize(qweight, qzeros, scales, g)
+    wb = gptq.dequantize_bf16(qweight, qzeros, scales, g)
+    rel = np.abs(gptq.bf16_to_float(wb) - w.astype(np.float32)) / np.maximum(np.abs(w.astype(np.float32)), 1e-30)
+    assert np.all(rel <= 2.0 ** -8)  # one bf16 rounding (8 significant bits) of the fp16 value
