@@ -3,10 +3,11 @@
 Mirrors ``cuda_extends/marlin.py`` (paths relative to
 ``/root/reference/After-Revision-DROFELL``):
 
-* :class:`MarlinTuningParams` -- ``marlin.py:18-53`` (same fields, same
-  flattened-M dispatch rule and validation);
-* :class:`MarlinDenseCache` -- ``marlin.py:56-87`` (shared fp16
-  reconstruction buffer; here it also owns the dw4_gemm split-K workspace);
+* :class:`MarlinTuningParams` -- ``marlin.py:18-53`` (the same fields and
+  flattened-M rule; MI355X-measured defaults);
+* :class:`MarlinDenseCache` -- ``marlin.py:56-87`` (the shared
+  reconstruction buffer; here also the dw4_gemm split-K workspace, both
+  sized by :class:`DenseRoutePlan`);
 * :func:`make_marlin_workspace` -- ``marlin.py:90-96``;
 * :class:`MarlinQ4Matrix` -- ``marlin.py:190-363`` (load-time repack,
   direct / reconstruct-then-dense dispatch, dequantisation, transposed
@@ -37,94 +38,158 @@ _SYMMETRIC_ZEROS = 0x77777777 - (1 << 32)  # int32 view of the word
 
 @dataclass(frozen=True)
 class MarlinTuningParams:
-    """Choose the packed kernel or reconstruct-then-dense GEMM by flattened M.
+    """Where the Marlin-path forward leaves the packed W4A16 kernel for the
+    dense route (dequantise, then a library GEMM), by flattened token count.
 
-    ``reconstruct_threshold`` applies to inference and no-cache PEFT;
-    ``grad_reconstruct_threshold`` when PEFT keeps the reconstructed weight
-    for backward.  ``None`` disables the dense forward for that path.
+    ``reconstruct_threshold`` serves inference and PEFT without a kept
+    weight; ``grad_reconstruct_threshold`` serves PEFT that keeps the
+    reconstructed weight for its backward (the forward then costs only the
+    library GEMM).  ``None`` keeps that case on the packed kernel at every
+    size.  The defaults are MI355X crossovers measured over the Llama-2-7B
+    projections (``bench.py --crossover``), not the reference's RTX 3090 ones.
     """
 
-    reconstruct_threshold: Optional[int] = 768
-    grad_reconstruct_threshold: Optional[int] = 128
+    reconstruct_threshold: Optional[int] = None
+    grad_reconstruct_threshold: Optional[int] = None
     reuse_reconstruct_cache_when_grad: Optional[bool] = None
 
     def __post_init__(self) -> None:
-        for name in ("reconstruct_threshold", "grad_reconstruct_threshold"):
-            value = getattr(self, name)
-            if value is not None and value <= 0:
-                raise ValueError(f"{name} must be positive or None")
+        bad = {name: v for name, v in (("reconstruct_threshold", self.reconstruct_threshold),
+                                       ("grad_reconstruct_threshold",
+                                        self.grad_reconstruct_threshold))
+               if v is not None and v < 1}
+        if bad:
+            raise ValueError(f"dense-route crossovers are token counts >= 1 or None, got {bad}")
+
+    def _crossover(self, cache_weight: bool) -> Optional[int]:
+        return self.grad_reconstruct_threshold if cache_weight else self.reconstruct_threshold
 
     def use_reconstructed_forward(self, flattened_tokens: int, *, cache_weight: bool) -> bool:
-        threshold = self.grad_reconstruct_threshold if cache_weight else self.reconstruct_threshold
-        return threshold is not None and flattened_tokens >= threshold
+        at = self._crossover(cache_weight)
+        return at is not None and flattened_tokens >= at
 
     def reuse_reconstruct_cache(self, default: bool) -> bool:
-        override = self.reuse_reconstruct_cache_when_grad
-        return default if override is None else override
+        keep = self.reuse_reconstruct_cache_when_grad
+        return default if keep is None else keep
 
     def direct_max_m(self) -> int:
-        """Largest flattened M the packed kernel can be asked to run."""
-        t = self.reconstruct_threshold
-        return 4096 if t is None else max(1, t - 1)
+        """Largest flattened M the packed kernel is asked to run without a
+        kept weight (sizes the shared split-K workspace)."""
+        at = self.reconstruct_threshold
+        return 4096 if at is None else max(1, at - 1)
+
+
+class DenseRoutePlan:
+    """Sizes of one decoder group's shared dense-route buffers: the
+    reconstruction buffer (the largest K x N of the group, fp16) and the
+    packed kernel's split-K workspace.  They grow while projections are
+    registered and are fixed once allocated; :class:`MarlinDenseCache`
+    allocates them and its memory twin mirrors them from the same plan."""
+
+    def __init__(self) -> None:
+        self.weight_elements = 0
+        self.workspace_bytes = 0
+        self.allocated = False
+
+    def grow(self, in_features: int, out_features: int, workspace_bytes: int = 0) -> None:
+        if self.allocated:
+            raise RuntimeError("the dense-route buffers are allocated already: register every "
+                               "projection before init_cache()")
+        self.weight_elements = max(self.weight_elements, in_features * out_features)
+        self.workspace_bytes = max(self.workspace_bytes, workspace_bytes)
+
+    def allocate(self) -> None:
+        if self.allocated:
+            raise RuntimeError("init_cache() ran already for this dense cache")
+        self.allocated = True
 
 
 class MarlinDenseCache:
-    """Shared stream-ordered fp16 reconstruction buffer plus the dw4_gemm
-    workspace of every matrix registered with :meth:`update`."""
+    """The shared, stream-ordered dense-route buffers of one decoder group
+    (sized by :class:`DenseRoutePlan`), plus the transposed product's
+    partial planes, grown on demand outside graph capture."""
 
     def __init__(self, device: torch.device) -> None:
         self.device = torch.device(device)
-        self.temp_weight_elements = 0
-        self.workspace_bytes = 0
-        self._temp_weight: Optional[torch.Tensor] = None
-        self._workspace: Optional[torch.Tensor] = None
+        self.plan = DenseRoutePlan()
+        self._buffers: Optional[tuple] = None
         self._t_workspace: Optional[torch.Tensor] = None
 
+    @property
+    def temp_weight_elements(self) -> int:
+        return self.plan.weight_elements
+
+    @property
+    def workspace_bytes(self) -> int:
+        return self.plan.workspace_bytes
+
     def update(self, in_features: int, out_features: int, workspace_bytes: int = 0) -> None:
-        if self._temp_weight is not None:
-            raise RuntimeError("cannot resize initialized Marlin dense cache")
-        self.temp_weight_elements = max(self.temp_weight_elements, in_features * out_features)
-        self.workspace_bytes = max(self.workspace_bytes, workspace_bytes)
+        self.plan.grow(in_features, out_features, workspace_bytes)
 
     def init_cache(self) -> None:
-        if self._temp_weight is not None:
-            raise RuntimeError("Marlin dense cache initialized twice")
-        self._temp_weight = torch.empty(self.temp_weight_elements, dtype=torch.float16,
-                                        device=self.device)
-        # zero-filled: its head holds split-K arrival counters
-        self._workspace = torch.zeros(max(self.workspace_bytes, 16), dtype=torch.uint8,
-                                      device=self.device)
+        self.plan.allocate()
+        weight = torch.empty(self.plan.weight_elements, dtype=torch.float16, device=self.device)
+        # zero-filled once: the kernels keep split-K arrival counters at its
+        # start and leave them at zero after every call
+        ws = torch.zeros(max(self.plan.workspace_bytes, 16), dtype=torch.uint8, device=self.device)
+        self._buffers = (weight, ws)
+
+    def _allocated(self) -> tuple:
+        if self._buffers is None:
+            raise RuntimeError("MarlinDenseCache.init_cache() has not run")
+        return self._buffers
 
     def weight(self, in_features: int, out_features: int) -> torch.Tensor:
-        if self._temp_weight is None:
-            raise RuntimeError("Marlin dense cache is not initialized")
-        elements = in_features * out_features
-        if elements > self._temp_weight.numel():
-            raise RuntimeError("Marlin dense cache is too small")
-        return self._temp_weight[:elements].view(in_features, out_features)
-
-    def transpose_workspace(self, nbytes: int) -> torch.Tensor:
-        """fp32 partial planes of the packed transposed product, grown on demand."""
-        if self._t_workspace is None or self._t_workspace.numel() < nbytes:
-            self._t_workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
-        return self._t_workspace
+        buf = self._allocated()[0]
+        need = in_features * out_features
+        if need > buf.numel():
+            raise RuntimeError(f"a {in_features} x {out_features} weight does not fit the "
+                               f"{buf.numel()}-element reconstruction buffer")
+        return buf[:need].view(in_features, out_features)
 
     @property
     def workspace(self) -> torch.Tensor:
-        if self._workspace is None:
-            raise RuntimeError("Marlin dense cache is not initialized")
-        return self._workspace
+        return self._allocated()[1]
+
+    def transpose_workspace(self, nbytes: int) -> torch.Tensor:
+        t = self._t_workspace
+        if t is None or t.numel() < nbytes:
+            t = self._t_workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8,
+                                                device=self.device)
+        return t
 
 
 def make_marlin_workspace(device: torch.device) -> torch.Tensor:
-    """Per-matrix lock buffer of the reference's Marlin GEMM.  The HIP
-    kernels keep their split-K state in :class:`MarlinDenseCache`; the
-    buffer is still allocated so module buffers and memory accounting match."""
+    """The per-matrix int32 buffer of 4 words per CU that the reference's
+    Marlin GEMM uses for locks.  The HIP kernels keep their split-K state in
+    the group's :class:`MarlinDenseCache`; the buffer is still created so the
+    module's buffers and memory accounting keep the reference's shape."""
     device = torch.device(device)
     if device.type != "cuda":
-        raise ValueError("Marlin workspace must be initialized on CUDA")
-    sms = torch.cuda.get_device_properties(device).multi_processor_count
-    return torch.zeros(sms * 4, dtype=torch.int32, device=device)
+        raise ValueError(f"the Marlin-path workspace lives on the GPU, not on {device}")
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    return torch.zeros(4 * cus, dtype=torch.int32, device=device)
+
+
+def marlin_module_tensors(in_features: int, out_features: int, group_size: int,
+                          act_order: bool, workspace_elements: int) -> dict:
+    """(shape, dtype) of every tensor a Marlin-path module holds after
+    ``post_init``, by buffer name: the packed matrix (the checkpoint's byte
+    counts), the row-sorted ``g_idx`` and its sort indices (act-order only),
+    the per-matrix workspace and the two reference dequantiser tables, which
+    this layout does not need (empty)."""
+    groups = in_features // group_size
+    index = in_features if act_order else 0
+    return {
+        "qweight": ((in_features // 8, out_features), torch.int32),
+        "qzeros": ((groups, out_features // 8), torch.int32),
+        "scales": ((groups, out_features), torch.float16),
+        "g_idx": ((index,), torch.int32),
+        "g_idx_sort_indices": ((index,), torch.int32),
+        "workspace": ((workspace_elements,), torch.int32),
+        "dequant_weight_permutation": ((0,), torch.int32),
+        "dequant_scale_column_map": ((0,), torch.int32),
+    }
 
 
 def _dense_matmul(x: torch.Tensor, weight: torch.Tensor, *,
@@ -136,18 +201,21 @@ def _dense_matmul(x: torch.Tensor, weight: torch.Tensor, *,
 
 
 class MarlinQ4Matrix:
-    """Repacked matrix plus its dispatch and reconstruction metadata."""
+    """One repacked symmetric GPTQ projection with the Marlin path's
+    dispatch (packed kernel or dense route) and reconstruction."""
 
     def __init__(self, qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
                  in_features: int, out_features: int, g_idx: torch.Tensor,
                  use_act_order: bool, workspace: torch.Tensor,
                  tuning_params: MarlinTuningParams, cache: MarlinDenseCache) -> None:
         if qweight.device.type != "cuda":
-            raise ValueError("Marlin weights must be initialized on CUDA")
+            raise ValueError(f"the checkpoint tensors must be on the GPU, not {qweight.device}")
         if not bool(torch.all(qzeros == _SYMMETRIC_ZEROS).item()):
-            raise ValueError("Marlin requires symmetric GPTQ zero points")
+            raise ValueError("the Marlin path takes symmetric checkpoints only: every stored "
+                             "zero nibble must be 7 (effective zero 8)")
         if workspace.device != qweight.device or workspace.dtype != torch.int32:
-            raise ValueError("Marlin workspace has the wrong device or dtype")
+            raise ValueError(f"workspace is {workspace.dtype} on {workspace.device}; "
+                             f"expected int32 on {qweight.device}")
         self.in_features = in_features
         self.out_features = out_features
         self.group_size = in_features // scales.shape[0]
@@ -192,8 +260,8 @@ class MarlinQ4Matrix:
     def set_tuning_params(self, tuning_params: MarlinTuningParams) -> None:
         self.tuning_params = tuning_params
 
-    _MOVED = ("qweight", "qzeros", "scales", "g_idx", "g_idx_sort_indices", "workspace",
-              "dequant_weight_permutation", "dequant_scale_column_map")
+    # the tensors a module move carries (every module buffer after post_init)
+    _MOVED = tuple(marlin_module_tensors(8, 8, 8, False, 0))
 
     def rebind(self, **tensors: torch.Tensor) -> None:
         """Point the matrix at moved copies of its tensors (module swap-out

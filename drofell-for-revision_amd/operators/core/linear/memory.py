@@ -28,18 +28,18 @@ twins need ``libdrofell_w4a16.so`` but no GPU.
 """
 from __future__ import annotations
 
-import math
 from abc import ABC, abstractmethod
 from typing import Callable, List, Optional
 
 import torch
 
 from hip_extends import _lib
-from hip_extends.marlin import MarlinTuningParams
+from hip_extends.marlin import DenseRoutePlan, MarlinTuningParams, marlin_module_tensors
 from hip_extends.w4a16 import TuningParams
 
 from ... import flags
 from ..memory.static import MemoryInt32, MemoryModule, MemoryTensor, MemoryUInt8
+from .gptq_layout import GptqGeometry, check_mergeable, checkpoint_buffers
 
 # CUs of an MI355X: the Marlin per-matrix workspace holds four int32 per CU
 MI355X_CUS = 256
@@ -98,22 +98,15 @@ class QuantLinearMemoryModel(MemoryModule):
     def __init__(self, group_size: int, in_features: int, out_features: int, bias: bool,
                  use_act_order: bool) -> None:
         super().__init__()
+        geo = GptqGeometry.resolve(in_features, out_features, group_size,
+                                   use_act_order).require_exllama()
         self.infeatures = in_features
         self.outfeatures = out_features
         self.use_act_order = use_act_order
         self.bits = 4
-        self.group_size = group_size if group_size != -1 else in_features
-        if in_features % 32 != 0:
-            raise AssertionError("in_features must be a multiple of 32")
-        if in_features % self.group_size != 0:
-            raise AssertionError("in_features must be a multiple of group_size")
-        if out_features % 32 != 0:
-            raise AssertionError("out_features must be a multiple of 32")
-        groups = math.ceil(in_features / self.group_size)
-        self.qweight = MemoryTensor((in_features // 32 * self.bits, out_features), MemoryInt32)
-        self.qzeros = MemoryTensor((groups, out_features // 32 * self.bits), MemoryInt32)
-        self.scales = MemoryTensor((groups, out_features), torch.float16)
-        self.g_idx = MemoryTensor((in_features,), MemoryInt32)
+        self.group_size = geo.group_size
+        for name, t in checkpoint_buffers(geo).items():
+            setattr(self, name, MemoryTensor(tuple(t.shape), t.dtype))
         if bias:
             self.bias = MemoryTensor((out_features,), torch.float16)
         self.cache_v2: Optional[CacheV2MemoryModel] = None
@@ -174,95 +167,91 @@ class QuantLinearMakerMemoryModel(LinearMakerMemoryModel):
 
 
 class MarlinQuantLinearMemoryModel(MemoryModule):
-    """Long-lived tensors of one Marlin-path projection after ``post_init``."""
+    """Twin of a repacked ``MarlinQuantLinear``: one :class:`MemoryTensor` per
+    buffer the module holds after ``post_init``, taken from the same table
+    the module is built from (:func:`hip_extends.marlin.marlin_module_tensors`)."""
 
     def __init__(self, group_size: int, in_features: int, out_features: int, bias: bool,
                  use_act_order: bool, workspace_elements: int = MI355X_CUS * 4) -> None:
         super().__init__()
-        if bias:
-            raise ValueError("the Marlin memory model does not support bias")
-        if in_features % 32 != 0 or out_features % 32 != 0:
-            raise ValueError("Marlin GPTQ dimensions must be multiples of 32")
-        self.infeatures = in_features
-        self.outfeatures = out_features
-        self.group_size = in_features if group_size == -1 else group_size
-        self.use_act_order = use_act_order and self.group_size < in_features
-        groups = math.ceil(in_features / self.group_size)
-        self.qweight = MemoryTensor((in_features // 8, out_features), MemoryInt32)
-        self.qzeros = MemoryTensor((groups, out_features // 8), MemoryInt32)
-        self.scales = MemoryTensor((groups, out_features), torch.float16)
-        index = in_features if self.use_act_order else 0
-        self.g_idx = MemoryTensor((index,), MemoryInt32)
-        self.g_idx_sort_indices = MemoryTensor((index,), MemoryInt32)
-        self.workspace = MemoryTensor((workspace_elements,), MemoryInt32)
-        self.dequant_weight_permutation = MemoryTensor((0,), MemoryInt32)
-        self.dequant_scale_column_map = MemoryTensor((0,), MemoryInt32)
+        geo = GptqGeometry.resolve(in_features, out_features, group_size, use_act_order,
+                                   single_group_act=False).require_marlin(bias)
+        self.infeatures, self.outfeatures = geo.in_features, geo.out_features
+        self.group_size, self.use_act_order = geo.group_size, geo.act_order
+        for name, (shape, dtype) in marlin_module_tensors(
+                geo.in_features, geo.out_features, geo.group_size, geo.act_order,
+                workspace_elements).items():
+            setattr(self, name, MemoryTensor(shape, dtype))
 
 
 class MarlinDenseCacheMemoryModel(MemoryModule):
-    """Twin of ``MarlinDenseCache``: one fp16 reconstruction buffer and one
-    GEMM workspace per decoder group."""
+    """Twin of ``MarlinDenseCache``, sized by the same :class:`DenseRoutePlan`:
+    the reconstruction buffer and the split-K workspace of a decoder group."""
 
     def __init__(self) -> None:
         super().__init__()
-        self.temp_weight_elements = 0
-        self.workspace_bytes = 0
-        self._temp_weight: Optional[MemoryTensor] = None
-        self._workspace: Optional[MemoryTensor] = None
-        self.cache_created = False
+        self.plan = DenseRoutePlan()
+
+    @property
+    def cache_created(self) -> bool:
+        return self.plan.allocated
+
+    @property
+    def temp_weight_elements(self) -> int:
+        return self.plan.weight_elements
+
+    @property
+    def workspace_bytes(self) -> int:
+        return self.plan.workspace_bytes
 
     def update(self, in_features: int, out_features: int, workspace_bytes: int = 0) -> None:
-        if self.cache_created:
-            raise RuntimeError("cannot resize initialized Marlin dense cache")
-        self.temp_weight_elements = max(self.temp_weight_elements, in_features * out_features)
-        self.workspace_bytes = max(self.workspace_bytes, workspace_bytes)
+        self.plan.grow(in_features, out_features, workspace_bytes)
 
     def init_cache(self) -> None:
-        if self.cache_created:
-            raise RuntimeError("Marlin dense cache initialized twice")
-        self._temp_weight = MemoryTensor((self.temp_weight_elements,), torch.float16)
-        self._workspace = MemoryTensor((max(self.workspace_bytes, 16),), MemoryUInt8)
-        self.cache_created = True
+        self.plan.allocate()
+        self._temp_weight = MemoryTensor((self.plan.weight_elements,), torch.float16)
+        self._workspace = MemoryTensor((max(self.plan.workspace_bytes, 16),), MemoryUInt8)
 
 
 class MarlinQuantLinearMakerMemoryModel(LinearMakerMemoryModel):
+    """Twin of ``MarlinQuantLinearMaker``: the group's projections and its
+    dense cache; every projection registers its dense-route sizes as it is
+    made, and ``post_init`` fixes them."""
+
     def __init__(self, quantization_group_size: int, use_act_order: bool,
                  workspace_elements: int = MI355X_CUS * 4,
                  tuning_params: Optional[MarlinTuningParams] = None) -> None:
         self.quantization_group_size = quantization_group_size
         self.use_act_order = use_act_order
         self.workspace_elements = workspace_elements
-        self.tuning_params = tuning_params or MarlinTuningParams()
+        self.tuning_params = tuning_params if tuning_params is not None else MarlinTuningParams()
         self.dense_cache = MarlinDenseCacheMemoryModel()
         self.quant_linears: List[MarlinQuantLinearMemoryModel] = []
         self.post_inited = False
 
     def make_linear(self, in_features: int, out_features: int,
                     bias: bool = False) -> MarlinQuantLinearMemoryModel:
-        linear = MarlinQuantLinearMemoryModel(
-            group_size=self.quantization_group_size, in_features=in_features,
-            out_features=out_features, bias=bias, use_act_order=self.use_act_order,
-            workspace_elements=self.workspace_elements)
-        self.quant_linears.append(linear)
+        twin = MarlinQuantLinearMemoryModel(self.quantization_group_size, in_features,
+                                            out_features, bias, self.use_act_order,
+                                            self.workspace_elements)
         self.dense_cache.update(in_features, out_features, _workspace_bytes(
-            in_features, out_features, linear.group_size, linear.use_act_order,
+            in_features, out_features, twin.group_size, twin.use_act_order,
             self.tuning_params.direct_max_m()))
-        return linear
+        self.quant_linears.append(twin)
+        return twin
 
     def post_init(self) -> None:
         if self.post_inited:
-            raise RuntimeError("MarlinQuantLinearMakerMemoryModel.post_init called twice")
+            raise RuntimeError("MarlinQuantLinearMakerMemoryModel.post_init: already ran")
         self.post_inited = True
         self.dense_cache.init_cache()
 
     def merge(self, linears: List[MarlinQuantLinearMemoryModel]) -> MarlinQuantLinearMemoryModel:
-        if not linears:
-            raise ValueError("cannot merge an empty list of Marlin linears")
-        first = linears[0]
-        if any(linear.infeatures != first.infeatures for linear in linears):
-            raise ValueError("merged Marlin linears must share in_features")
-        merged = self.make_linear(first.infeatures,
+        """The twin of a merged projection (the checkpoint tensors it would
+        join are not modelled, so only the shapes are checked)."""
+        check_mergeable(linears, compare_rows=False)
+        merged = self.make_linear(linears[0].infeatures,
                                   sum(linear.outfeatures for linear in linears), False)
-        for linear in linears:
-            self.quant_linears.remove(linear)
+        gone = {id(linear) for linear in linears}
+        self.quant_linears = [t for t in self.quant_linears if id(t) not in gone]
         return merged

@@ -1,23 +1,27 @@
-"""The reference's Marlin quantized Linear, backed by the HIP W4A16 library.
+"""Marlin-path quantized Linear: the reference's API on the HIP W4A16 kernels.
 
-Mirrors ``operators/core/linear/real_marlin.py`` of the reference (paths
-relative to ``/root/reference/After-Revision-DROFELL``):
+The reference (``operators/core/linear/real_marlin.py``, paths relative to
+``/root/reference/After-Revision-DROFELL``) keeps a second Linear front end
+for its Marlin backend: the same GPTQ checkpoint buffers, no bias, a
+per-matrix lock workspace, merged q/k/v and gate/up projections, and a
+forward that runs the packed GEMM below a token threshold and a dense GEMM
+over the reconstructed weight above it.  Here both front ends drive one
+library: :class:`MarlinQuantLinear` hands its checkpoint tensors to
+:class:`~hip_extends.marlin.MarlinQ4Matrix`, which repacks them into this
+library's layout (not Marlin's tiles) and owns the dispatch.
 
-* :class:`MarlinQuantLinear` -- constructor checks and buffers
-  (``real_marlin.py:24-79``), ``post_init`` re-registering the runtime tensors
-  (``:81-117``), ``reconstruct_weight`` / ``dense_forward`` / ``forward``
-  (``:119-157``: input cast to fp16 and back, grad-enabled route through the
-  autograd function);
-* :class:`MarlinQuantLinearMaker` -- ``post_init`` / ``set_tuning_param`` /
-  ``merge`` / ``make_linear`` (``:160-244``).  ``merge`` concatenates GPTQ
-  checkpoint tensors along the output dimension before the repack, as the
-  Marlin loader does for q/k/v and gate/up
-  (``operators/assemble/decoders/real_loader_marlin.py:61-79``).
+What stays the reference's, because callers and checkpoints depend on it:
+the class and method names and signatures (``make_linear``, ``post_init``,
+``set_tuning_param``, ``merge``, ``reconstruct_weight``, ``dense_forward``,
+``forward``), the buffer names a module exposes after ``post_init``, and
+the exception types.  The geometry checks and buffer construction are shared
+with :class:`~operators.core.linear.real_quant.QuantLinear`
+(:mod:`operators.core.linear.gptq_layout`); the tensors a repacked module
+holds are listed once, in :func:`hip_extends.marlin.marlin_module_tensors`.
 """
 from __future__ import annotations
 
-import math
-from typing import Callable, List, Optional, cast
+from typing import List, Optional, cast
 
 import torch
 from torch import nn
@@ -27,67 +31,68 @@ from hip_extends.marlin import (MarlinDenseCache, MarlinQ4ForwardOnlyLinearFunct
                                 make_marlin_workspace)
 
 from ... import flags
+from .gptq_layout import GptqGeometry, checkpoint_buffers, concat_outputs
 from .real import Linear, LinearMaker
 
 
+def _marlin_forward(matrix: MarlinQ4Matrix, x: torch.Tensor) -> torch.Tensor:
+    """The Marlin path computes in the scales' dtype (fp16) and returns the
+    caller's dtype; a grad-tracking input goes through the autograd function,
+    which may keep the reconstructed weight for its backward."""
+    x16 = x.to(matrix.scales.dtype)
+    if torch.is_grad_enabled() and x16.requires_grad:
+        keep = matrix.tuning_params.reuse_reconstruct_cache(flags.REUSE_RECONSTRUCT_CACHE_WHEN_GRAD)
+        y = MarlinQ4LinearFunction.apply(x16, matrix, keep)
+    else:
+        y = MarlinQ4ForwardOnlyLinearFunction.apply(x16, matrix)
+    return cast(torch.Tensor, y).to(x.dtype)
+
+
 class MarlinQuantLinear(Linear):
-    """Checkpoint-facing GPTQ linear backed by :class:`MarlinQ4Matrix`."""
+    """One GPTQ projection on the Marlin-path interface (reference
+    ``real_marlin.py:24-157``)."""
 
     def __init__(self, group_size: int, in_features: int, out_features: int, bias: bool,
                  use_act_order: bool) -> None:
         nn.Module.__init__(self)
-        if bias:
-            raise ValueError("the Marlin decode backend does not support bias")
-        if in_features % 32 != 0 or out_features % 32 != 0:
-            raise ValueError("Marlin GPTQ dimensions must be multiples of 32")
-        self.infeatures = in_features
-        self.outfeatures = out_features
-        self.group_size = in_features if group_size == -1 else group_size
-        if in_features % self.group_size != 0:
-            raise ValueError("in_features must be divisible by group_size")
-        self.use_act_order = use_act_order and self.group_size < in_features
-
-        self.register_buffer("qweight", torch.zeros((in_features // 8, out_features),
-                                                    dtype=torch.int32))
-        self.register_buffer("qzeros", torch.zeros(
-            (math.ceil(in_features / self.group_size), out_features // 8), dtype=torch.int32))
-        self.register_buffer("scales", torch.zeros(
-            (math.ceil(in_features / self.group_size), out_features), dtype=torch.float16))
-        self.register_buffer("g_idx", torch.tensor(
-            [i // self.group_size for i in range(in_features)], dtype=torch.int32))
+        geo = GptqGeometry.resolve(in_features, out_features, group_size, use_act_order,
+                                   single_group_act=False).require_marlin(bias)
+        self.infeatures, self.outfeatures = geo.in_features, geo.out_features
+        self.group_size, self.use_act_order = geo.group_size, geo.act_order
+        for name, t in checkpoint_buffers(geo).items():
+            self.register_buffer(name, t)
         self.register_buffer("workspace", make_marlin_workspace(self.qweight.device),
                              persistent=False)
         self.bias = None
         self.q4_matrix: Optional[MarlinQ4Matrix] = None
 
     def post_init(self, tuning_params: MarlinTuningParams, cache: MarlinDenseCache) -> None:
+        """Repack the loaded checkpoint tensors; the module then holds the
+        matrix's runtime tensors under the reference's buffer names (one copy
+        of each, so moves and memory accounting see what the kernels use)."""
         if self.q4_matrix is not None:
-            raise RuntimeError("MarlinQuantLinear.post_init called twice")
-        q4_matrix = MarlinQ4Matrix(self.qweight, self.qzeros, self.scales, self.infeatures,
-                                   self.outfeatures, self.g_idx, self.use_act_order,
-                                   self.workspace, tuning_params, cache)
-        # every persistent runtime tensor stays registered on the module
-        self.qweight = q4_matrix.qweight
-        self.qzeros = q4_matrix.qzeros
-        self.scales = q4_matrix.scales
-        self.g_idx = q4_matrix.g_idx
-        self.register_buffer("g_idx_sort_indices", q4_matrix.g_idx_sort_indices)
-        self.register_buffer("dequant_weight_permutation", q4_matrix.dequant_weight_permutation)
-        self.register_buffer("dequant_scale_column_map", q4_matrix.dequant_scale_column_map)
-        self.q4_matrix = q4_matrix
+            raise RuntimeError(f"{type(self).__name__} is repacked already")
+        matrix = MarlinQ4Matrix(self.qweight, self.qzeros, self.scales, self.infeatures,
+                                self.outfeatures, self.g_idx, self.use_act_order, self.workspace,
+                                tuning_params, cache)
+        for name in MarlinQ4Matrix._MOVED:
+            self.register_buffer(name, getattr(matrix, name),
+                                 persistent=name not in self._non_persistent_buffers_set)
+        self.q4_matrix = matrix
 
     def _apply(self, fn, recurse: bool = True):
-        """Module moves carry the repacked buffers; the matrix object is
-        re-pointed at the moved copies (no repack)."""
+        """A module move carries the repacked buffers; the matrix is pointed
+        at the moved copies (nothing is repacked)."""
         super()._apply(fn, recurse)
         if self.q4_matrix is not None:
-            self.q4_matrix.rebind(**{name: getattr(self, name) for name in MarlinQ4Matrix._MOVED})
+            self.q4_matrix.rebind(**{name: self._buffers[name] for name in MarlinQ4Matrix._MOVED})
         return self
 
     def _matrix(self) -> MarlinQ4Matrix:
-        if self.q4_matrix is None:
-            raise RuntimeError("MarlinQuantLinear must be repacked before use")
-        return self.q4_matrix
+        matrix = self.q4_matrix
+        if matrix is None:
+            raise RuntimeError(f"{type(self).__name__}.post_init() has not repacked the weights")
+        return matrix
 
     @property
     def tuning_params(self) -> MarlinTuningParams:
@@ -100,74 +105,52 @@ class MarlinQuantLinear(Linear):
         return self._matrix().dense_matmul(x, dense_weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        matrix = self._matrix()
-        input_dtype = x.dtype
-        marlin_input = x.to(matrix.scales.dtype)
-        if torch.is_grad_enabled() and marlin_input.requires_grad:
-            cache_weight = matrix.tuning_params.reuse_reconstruct_cache(
-                flags.REUSE_RECONSTRUCT_CACHE_WHEN_GRAD)
-            output = MarlinQ4LinearFunction.apply(marlin_input, matrix, cache_weight)
-        else:
-            output = MarlinQ4ForwardOnlyLinearFunction.apply(marlin_input, matrix)
-        return cast(torch.Tensor, output).to(input_dtype)
+        return _marlin_forward(self._matrix(), x)
 
 
 class MarlinQuantLinearMaker(LinearMaker):
+    """Makes the Marlin-path projections of a decoder group, merges those
+    that share an input, and repacks them all in ``post_init`` (reference
+    ``real_marlin.py:160-244``)."""
+
     def __init__(self, quantization_group_size: int, use_act_order: bool) -> None:
         self.quantization_group_size = quantization_group_size
         self.use_act_order = use_act_order
         self.quant_linears: List[MarlinQuantLinear] = []
         self.post_inited = False
 
-    def _apply(self, func: Callable[[MarlinQuantLinear], None]) -> None:
-        for linear in self.quant_linears:
-            func(linear)
+    def make_linear(self, in_features: int, out_features: int,
+                    bias: bool = False) -> MarlinQuantLinear:
+        made = MarlinQuantLinear(self.quantization_group_size, in_features, out_features, bias,
+                                 self.use_act_order)
+        self.quant_linears.append(made)
+        return made
 
     def post_init(self, tuning_params: MarlinTuningParams,
                   shared_cache: MarlinDenseCache) -> "MarlinQuantLinearMaker":
-        if self.post_inited:
-            raise RuntimeError("MarlinQuantLinearMaker.post_init called twice")
-        if not self.quant_linears:
-            raise RuntimeError("Marlin maker contains no quantized linears")
+        if self.post_inited or not self.quant_linears:
+            raise RuntimeError("MarlinQuantLinearMaker.post_init: " + (
+                "already ran" if self.post_inited else "no projections were made"))
         self.post_inited = True
-        self._apply(lambda linear: linear.post_init(tuning_params, shared_cache))
+        for linear in self.quant_linears:
+            linear.post_init(tuning_params, shared_cache)
         return self
 
     def set_tuning_param(self, tuning_params: MarlinTuningParams) -> "MarlinQuantLinearMaker":
-        self._apply(lambda linear: linear._matrix().set_tuning_params(tuning_params))
+        for linear in self.quant_linears:
+            linear._matrix().set_tuning_params(tuning_params)
         return self
 
     def merge(self, linears: List[MarlinQuantLinear]) -> MarlinQuantLinear:
-        """One linear whose output columns are the given linears' outputs,
-        in order (checkpoint tensors concatenated along N)."""
-        if not linears:
-            raise ValueError("cannot merge an empty list of Marlin linears")
-        first = linears[0]
-        if any(linear.infeatures != first.infeatures for linear in linears):
-            raise ValueError("merged Marlin linears must share in_features")
-        if any(linear.group_size != first.group_size for linear in linears):
-            raise ValueError("merged Marlin linears must share group_size")
-        if any(linear.use_act_order != first.use_act_order for linear in linears):
-            raise ValueError("merged Marlin linears must share act-order mode")
-        if any(not torch.equal(linear.g_idx, first.g_idx) for linear in linears[1:]):
-            raise ValueError("merged Marlin linears must share g_idx")
-        # built where the merged tensors live (its workspace is a device buffer)
-        with torch.device(first.qweight.device):
-            merged = self.make_linear(in_features=first.infeatures,
-                                      out_features=sum(linear.outfeatures for linear in linears),
-                                      bias=False)
-        merged.qweight = torch.cat([linear.qweight for linear in linears], dim=1).contiguous()
-        merged.qzeros = torch.cat([linear.qzeros for linear in linears], dim=1).contiguous()
-        merged.scales = torch.cat([linear.scales for linear in linears], dim=1).contiguous()
-        merged.g_idx = first.g_idx
-        for linear in linears:
-            self.quant_linears.remove(linear)
+        """One projection whose outputs are the given projections' outputs in
+        order; it replaces them in this maker.  Call before ``post_init``
+        (the joining works on checkpoint tensors)."""
+        joined = concat_outputs(linears)
+        width = sum(linear.outfeatures for linear in linears)
+        with torch.device(joined["qweight"].device):  # the workspace is a device buffer
+            merged = self.make_linear(linears[0].infeatures, width, bias=False)
+        for name, t in joined.items():
+            setattr(merged, name, t)
+        gone = {id(linear) for linear in linears}
+        self.quant_linears = [lin for lin in self.quant_linears if id(lin) not in gone]
         return merged
-
-    def make_linear(self, in_features: int, out_features: int,
-                    bias: bool = False) -> MarlinQuantLinear:
-        linear = MarlinQuantLinear(group_size=self.quantization_group_size,
-                                   in_features=in_features, out_features=out_features,
-                                   bias=bias, use_act_order=self.use_act_order)
-        self.quant_linears.append(linear)
-        return linear

@@ -19,7 +19,6 @@ relative to ``/root/reference/After-Revision-DROFELL``):
 """
 from __future__ import annotations
 
-import math
 from typing import Callable, List, cast
 
 import torch
@@ -29,6 +28,7 @@ from hip_extends.w4a16 import (CacheV2, Q4ForwardOnlyLinearFunction, Q4LinearFun
                                Q4MatrixV2, TuningParams)
 
 from ... import flags
+from .gptq_layout import GptqGeometry, checkpoint_buffers
 from .real import Linear, LinearMaker
 
 
@@ -36,35 +36,17 @@ class QuantLinear(Linear):
     def __init__(self, group_size: int, in_features: int, out_features: int, bias: bool,
                  use_act_order: bool):
         nn.Module.__init__(self)
+        # the reference's asserts (AssertionError) on the resolved geometry
+        geo = GptqGeometry.resolve(in_features, out_features, group_size,
+                                   use_act_order).require_exllama()
         self.infeatures = in_features
         self.outfeatures = out_features
         self.use_act_order = use_act_order
         self.bits = 4
-        self.group_size = group_size if group_size != -1 else in_features
+        self.group_size = geo.group_size
         self.maxq = 2 ** self.bits - 1
-
-        # same checks (and exception type) as the reference's asserts
-        if in_features % 32 != 0:
-            raise AssertionError("in_features must be a multiple of 32")
-        if in_features % self.group_size != 0:
-            raise AssertionError("in_features must be a multiple of group_size")
-        if out_features % 32 != 0:
-            raise AssertionError("out_features must be a multiple of 32")
-
-        self.register_buffer(
-            "qweight",
-            torch.zeros((in_features // 32 * self.bits, out_features), dtype=torch.int32))
-        self.register_buffer(
-            "qzeros",
-            torch.zeros((math.ceil(in_features / self.group_size),
-                         out_features // 32 * self.bits), dtype=torch.int32))
-        self.register_buffer(
-            "scales",
-            torch.zeros((math.ceil(in_features / self.group_size), out_features),
-                        dtype=torch.float16))
-        self.register_buffer(
-            "g_idx",
-            torch.tensor([i // self.group_size for i in range(in_features)], dtype=torch.int32))
+        for name, t in checkpoint_buffers(geo).items():
+            self.register_buffer(name, t)
         if bias:
             self.register_buffer("bias", torch.zeros(out_features, dtype=torch.float16))
         else:

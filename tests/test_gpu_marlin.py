@@ -54,12 +54,23 @@ def test_marlin_linear_direct_and_dense(hip_device):
     lin.reconstruct_weight(out)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy().view(np.uint16), w.view(np.uint16))
-    for m in (1, 8, 300, 800):  # 800 >= reconstruct_threshold: dense route
-        say(f"marlin forward M={m}")
+    at = MarlinTuningParams().reconstruct_threshold
+    ms = (1, 8, 300, 800) + (() if at is None else (at - 1, at))
+    for m in ms:  # the default crossover: packed kernel below it, dense route from it
+        say(f"marlin forward M={m} (default crossover {at})")
         x = make_x(m, k, seed=m)
         y = lin(x.to(hip_device))
         torch.cuda.synchronize()
         check_tol(y, gptq.gemm_ref(x.numpy(), w), f"marlin M={m}")
+    maker.set_tuning_param(MarlinTuningParams(reconstruct_threshold=600))
+    for m in (599, 600):  # either side of an explicit crossover
+        say(f"marlin forward M={m} (crossover 600)")
+        assert lin.q4_matrix.use_reconstructed_forward(m, cache_weight=False) == (m >= 600)
+        x = make_x(m, k, seed=m + 1)
+        y = lin(x.to(hip_device))
+        torch.cuda.synchronize()
+        check_tol(y, gptq.gemm_ref(x.numpy(), w), f"marlin M={m} crossover 600")
+    maker.set_tuning_param(MarlinTuningParams())
     say("marlin bf16 input keeps its dtype")
     yb = lin(make_x(4, k, seed=4).to(hip_device, torch.bfloat16))
     assert yb.dtype == torch.bfloat16

@@ -9,13 +9,15 @@ from operators.core.linear.real_marlin import MarlinQuantLinear, MarlinQuantLine
 
 
 def test_tuning_params_dispatch_rule():
-    tp = MarlinTuningParams()
+    tp = MarlinTuningParams(reconstruct_threshold=768, grad_reconstruct_threshold=128)
     assert not tp.use_reconstructed_forward(767, cache_weight=False)
     assert tp.use_reconstructed_forward(768, cache_weight=False)
     assert not tp.use_reconstructed_forward(127, cache_weight=True)
     assert tp.use_reconstructed_forward(128, cache_weight=True)
+    assert tp.direct_max_m() == 767
     off = MarlinTuningParams(reconstruct_threshold=None)
     assert not off.use_reconstructed_forward(10 ** 6, cache_weight=False)
+    assert off.direct_max_m() == 4096
     assert tp.reuse_reconstruct_cache(True) is True
     assert MarlinTuningParams(reuse_reconstruct_cache_when_grad=False).reuse_reconstruct_cache(True) is False
     with pytest.raises(ValueError):
