@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <vector>
 
 #include "drofell_w4a16.h"
@@ -161,6 +162,7 @@ const char* dw4_strerror(int status) {
     case DW4_ERR_WORKSPACE: return "workspace too small for this call (see dw4_workspace_size)";
     case DW4_ERR_LAUNCH: return "kernel launch failed";
     case DW4_ERR_DEVICE: return "HIP device error";
+    case DW4_ERR_SCRATCH: return "call needs more scratch than dw4_gemm_noalloc's fixed DW4_NOALLOC_SCRATCH_BYTES (use dw4_gemm with a workspace of dw4_workspace_size bytes)";
     default: return "unknown status";
   }
 }
@@ -830,3 +832,71 @@ int dw4_decoder_after_stage(int m, const uint16_t* attn, int64_t lda, const uint
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// dw4_gemm_noalloc: dw4_gemm on a file-scope scratch array instead of a
+// caller workspace.  The array's name is a host-side stand-in; kernels get the
+// device address from hipGetSymbolAddress, looked up once per device.
+// ---------------------------------------------------------------------------
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[DW4_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mutex;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+__global__ void clear_words_kernel(uint32_t* __restrict__ p, int words) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < words) p[i] = 0u;
+}
+
+// The current device's scratch address (null on failure, with *status set).
+// The first call on a device also clears the arrival-counter head with a fill
+// kernel on `stream` (no memset node, so a capturing caller's graph stays
+// free of them); every later call leaves the head at zero.
+void* scratch_for_current_device(hipStream_t stream, int* status) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *status = DW4_ERR_DEVICE;
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return p;
+  void* addr = nullptr;
+  if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) {
+    *status = DW4_ERR_DEVICE;
+    return nullptr;
+  }
+  constexpr int words = (int)(dw4::kWsHeadBytes / sizeof(uint32_t));
+  clear_words_kernel<<<(words + 255) / 256, 256, 0, stream>>>(static_cast<uint32_t*>(addr), words);
+  if (hipGetLastError() != hipSuccess) {
+    *status = DW4_ERR_LAUNCH;
+    return nullptr;
+  }
+  g_scratch_ptr[dev].store(addr, std::memory_order_release);
+  return addr;
+}
+
+}  // namespace
+
+extern "C" int dw4_gemm_noalloc(int m, int k, int n, int group_size, const uint16_t* x,
+                                int64_t ldx, const int32_t* packed_qweight,
+                                const int32_t* packed_zeros, const uint16_t* packed_scales,
+                                const int32_t* perm, const uint16_t* bias, uint16_t* y,
+                                int64_t ldy, void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (m < 0) return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  const size_t need = workspace_for(DW4_PATH_AUTO, m, k, n, group_size, perm != nullptr);
+  if (need > DW4_NOALLOC_SCRATCH_BYTES) return DW4_ERR_SCRATCH;
+  int status = DW4_OK;
+  void* ws = scratch_for_current_device(static_cast<hipStream_t>(stream), &status);
+  if (ws == nullptr) return status;
+  return gemm_run(DW4_PATH_AUTO, 0, m, k, n, group_size, x, ldx, packed_qweight, packed_zeros,
+                  packed_scales, perm, bias, y, ldy, nullptr, 0, ws, DW4_NOALLOC_SCRATCH_BYTES,
+                  stream);
+}

@@ -22,6 +22,8 @@ DW4_ERR_BAD_GIDX = 4
 DW4_ERR_WORKSPACE = 5
 DW4_ERR_LAUNCH = 6
 DW4_ERR_DEVICE = 7
+DW4_ERR_SCRATCH = 8
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 DW4_PATH_AUTO = 0
 DW4_PATH_DECODE = 1
@@ -58,6 +60,8 @@ SIGNATURES = {
                                  _P, _c.c_size_t, _P]),
     "dw4_dequant": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
                                _c.c_int64, _P]),
+    "dw4_gemm_noalloc": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64,
+                                    _P, _P, _P, _P, _P, _P, _c.c_int64, _P]),
     "dw4_dequant_bf16": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P,
                                     _c.c_int64, _P]),
     "dw4_stream_read": (_c.c_int, [_P, _c.c_size_t, _c.c_int, _c.c_int, _c.c_uint32, _P, _P]),

@@ -45,10 +45,11 @@
  *   - Every function returns an int status (DW4_OK == 0); no exception or
  *     abort crosses the ABI.  dw4_strerror() names a status.
  *   - Every buffer is owned by the caller.  The library allocates nothing
- *     on the device, keeps no pointer after a call returns and holds no
- *     global mutable state except per-device records: the CU count and,
- *     per kernel, whether its dynamic LDS limit has been raised on that
- *     device.
+ *     on the device (beyond dw4_gemm_noalloc's fixed scratch array, which
+ *     the code object carries), keeps no pointer after a call returns and
+ *     holds no global mutable state except per-device records: the CU
+ *     count, per kernel whether its dynamic LDS limit has been raised on
+ *     that device, and the address of that device's scratch array.
  *   - Device pointers refer to memory of the current HIP device; `stream`
  *     is a hipStream_t (NULL = the null stream).  Work is enqueued on it.
  *   - dw4_gemm never synchronises, never allocates and launches a fixed
@@ -109,7 +110,8 @@ enum {
   DW4_ERR_BAD_GIDX = 4,      /* g_idx out of range or groups not uniform */
   DW4_ERR_WORKSPACE = 5,     /* workspace smaller than dw4_workspace_size() */
   DW4_ERR_LAUNCH = 6,        /* a kernel launch failed (hipGetLastError) */
-  DW4_ERR_DEVICE = 7         /* no usable HIP device / runtime error */
+  DW4_ERR_DEVICE = 7,        /* no usable HIP device / runtime error */
+  DW4_ERR_SCRATCH = 8        /* dw4_gemm_noalloc: the call needs more than its fixed scratch */
 };
 
 /* Path selection for dw4_gemm_path(). */
@@ -168,6 +170,24 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size,
                   const uint16_t* packed_scales, const int32_t* perm,
                   const uint16_t* bias, uint16_t* y, int64_t ldy,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* dw4_gemm for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same arguments and results as dw4_gemm without the
+ * workspace: the split-K partials, arrival counters and gathered act-order
+ * activations live in one file-scope device array of
+ * DW4_NOALLOC_SCRATCH_BYTES per GPU (held from the library's first use on
+ * that GPU until the process ends).  A call whose dw4_workspace_size exceeds
+ * that returns DW4_ERR_SCRATCH before launching anything.  Every call on a
+ * GPU shares that GPU's array, so calls that overlap in time on one GPU
+ * (concurrent streams or threads) race; serialise them.  Calls no hipMalloc,
+ * hipFree or allocating library routine. */
+#define DW4_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int dw4_gemm_noalloc(int m, int k, int n, int group_size,
+                     const uint16_t* x, int64_t ldx,
+                     const int32_t* packed_qweight, const int32_t* packed_zeros,
+                     const uint16_t* packed_scales, const int32_t* perm,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, void* stream);
 
 /* Device: dequantised fp16 weight w[K, N] (row stride ldw) in ORIGINAL row
  * order, bit-exact with fp16_rne(scale * (q - (zero + 1))). */

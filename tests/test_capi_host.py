@@ -36,9 +36,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_strerror_names_every_status():
-    msgs = {s: _lib.strerror(s) for s in range(8)}
+    msgs = {s: _lib.strerror(s) for s in range(9)}
     assert msgs[0] == "ok"
-    assert len(set(msgs.values())) == 8
+    assert len(set(msgs.values())) == 9
     assert _lib.strerror(99) == "unknown status"
 
 
