@@ -67,10 +67,10 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n);
 // split count: with too little workspace the call runs unsplit.
 dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_bytes, bool cap_by_ws) {
   dw4::PrefillPlan p;
-  // Row tile: 16 or 32 rows just covering small M, then 64 or 128.  Fewer
-  // rows per tile mean fewer MFMA uses per dequantised weight fragment, so
-  // the small tiles are only for small M.
-  p.bm = m <= 16 ? 16 : m <= 32 ? 32 : m < dw4::kPrefillBm128MinM ? 64 : 128;
+  // Row tile: 16 or 32 rows just covering small M, then 64 (above 128 rows
+  // the choice below).  Fewer rows per tile mean fewer MFMA uses per
+  // dequantised weight fragment, so the small tiles are only for small M.
+  p.bm = m <= 16 ? 16 : m <= 32 ? 32 : 64;
   p.bn = n >= 2048 ? 256 : 128;
   const int kc = k / kChunkK;
   const int cus_now = cu_count();
@@ -92,20 +92,34 @@ dw4::PrefillPlan plan_prefill(int m, int k, int n, int split_req, size_t ws_byte
     p.bn = 128;
     if (p.bm == 64 && m <= 64 && filled(32, 128) > filled(64, 128)) p.bm = 32;
   }
-  // 128-row tiles reuse each dequantised weight fragment twice as often
-  // (measured ~44% vs ~33% of a CU's MFMA peak) but halve the tile count:
-  // take them wherever 64-row tiles would need more than one round of
-  // workgroups (one per CU) and 128-row tiles need only one.
-  if (p.bm == 64) {
-    const int nt = (n + p.bn - 1) / p.bn;
-    if (((m + 63) / 64) * nt > cus_now && ((m + 127) / 128) * nt <= cus_now) p.bm = 128;
+  // Above 128 rows, the LDS-streamed kernel, on the tile shape that needs
+  // the fewest rounds of workgroups (one workgroup per CU at a time), ties
+  // going to the first of: 64 x 256 (up to 512 rows: twice the tiles of
+  // 128-row ones, so fewer split-K partial planes), 128 x 128, 128 x 256
+  // (each dequantised weight fragment feeds four MFMAs in the 128-row
+  // tiles).  Measured (us): 4096^2 M=512 30.8 with 64 x 256 against 35.1
+  // with 128 x 128; 4096x11008 M=512 74.4 with two rounds of 64 x 256
+  // against 61.3 with one of 128 x 256; 4096^2 M=1024 42.0 with 128 x 128
+  // against 52.9 with 64 x 256.
+  if (m > 128) {
+    const int cand[3][2] = {{64, 256}, {128, 128}, {128, 256}};
+    int best_rounds = 1 << 30;
+    for (int c = m <= 512 ? 0 : 1; c < 3; ++c) {
+      const int t = ((m + cand[c][0] - 1) / cand[c][0]) * ((n + cand[c][1] - 1) / cand[c][1]);
+      const int rounds = (t + cus_now - 1) / cus_now;
+      if (rounds < best_rounds) {
+        best_rounds = rounds;
+        p.bm = cand[c][0];
+        p.bn = cand[c][1];
+      }
+    }
   }
   const int tiles = ((m + p.bm - 1) / p.bm) * ((n + p.bn - 1) / p.bn);
   // Automatic splits: enough to give every CU a workgroup (one per CU at a
-  // time), with at least 8 chunks per split and at most 8 splits: the last
-  // split of a tile to arrive sums all the others' partials, so more splits
-  // lengthen that tail faster than they add parallelism (measured on 7B
-  // shapes).
+  // time), with at least 8 chunks per split and at most 8 splits: every
+  // split adds a partial plane to write and sum (the LDS-streamed kernel) or
+  // lengthens the last-arriving split's sum (the kernel below 129 rows)
+  // faster than it adds parallelism (measured on 7B shapes).
   int splits = split_req > 0 ? split_req : auto_splits(tiles);
   splits = std::max(1, std::min(splits, kc));
   // the launcher rounds to whole chunks per split
@@ -314,6 +328,11 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
   if (plan.splits > 1 && !aligned16(workspace)) plan.splits = 1;
   const int e = gather_after(plan.splits > 1 ? prefill_ws_bytes(plan, m, n) : 0);
   if (e != DW4_OK) return e;
+  // above 128 rows the LDS-streamed kernel, which needs x in the packed row
+  // order (act-order calls whose workspace could not hold the gathered rows
+  // keep the kernel that gathers per workgroup)
+  if (m > 128 && a.perm == nullptr)
+    return status_of(dw4::launch_prefill2(a, plan, workspace, s));
   return status_of(dw4::launch_prefill(a, plan, workspace, s));
 }
 

@@ -62,6 +62,24 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Two 16-column strips' packed word w (lanes L: column L%16, rows 8(L/16)..)
+// rearranged into the B operands of v_mfma_f32_32x32x16_f16 for the strip
+// pair's 32 columns: `even` holds k-step 2w (lane L: column L%32, rows
+// 8(L/32)..), `odd` k-step 2w+1.
+__device__ __forceinline__ void strip_pair_to_b32(uint32_t a, uint32_t b, uint32_t& even,
+                                                  uint32_t& odd) {
+  const auto x = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  const auto y = __builtin_amdgcn_permlane32_swap(x[0], x[1], false, false);
+  even = y[0];
+  odd = y[1];
+}
+
 // One 16-byte unit (8 consecutive sorted rows) of an activation row,
 // gathered through perm for act-order checkpoints.
 template <bool ACT>

@@ -79,7 +79,6 @@ struct Items {
 struct PrefillPlan {
   int bm, bn, splits;
 };
-constexpr int kPrefillBm128MinM = 513;  // smallest M that gets 128-row prefill tiles
 
 struct DecodePlan {
   int splits;   // workgroups along K per strip
@@ -203,6 +202,16 @@ inline size_t split_ws_bytes(int splits, size_t plane_floats) {
 
 hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* ws,
                           hipStream_t stream);
+// y[m][n] = fp16(sum over s < splits, in order, of part[s][m][n] (+ bias[n]))
+// (+ res[m][n]): the split-K planes [splits][M][N] of one product.
+hipError_t launch_reduce_planes(const float* part, int splits, int M, int N, const uint16_t* bias,
+                                uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldres,
+                                hipStream_t stream);
+// The LDS-streamed prefill kernel (w4a16_prefill.hip): 64 x 256, 128 x 128 or
+// 128 x 256 tiles, x already in the packed row order (perm null).  Split-K partial planes
+// [splits][M][N] after the workspace head, summed by launch_reduce_planes.
+hipError_t launch_prefill2(const GemmArgs& a, const PrefillPlan& plan, void* ws,
+                           hipStream_t stream);
 hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,
                           const int32_t* perm, uint16_t* w, int64_t ldw, int K, int N, int gs,
                           int G, hipStream_t stream);

@@ -1037,19 +1037,6 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 // Accumulator element i of lane L is row 8(i/4) + 4(L/32) + i%4, column
 // L%32 of the 32x32 tile.
 // ---------------------------------------------------------------------------
-typedef float f16v __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ void strip_pair_to_b32(uint32_t a, uint32_t b, uint32_t& even,
-                                                  uint32_t& odd) {
-  const auto x = __builtin_amdgcn_permlane16_swap(a, b, false, false);
-  const auto y = __builtin_amdgcn_permlane32_swap(x[0], x[1], false, false);
-  even = y[0];
-  odd = y[1];
-}
 
 template <int MT3, int P, int PB, int GPC, bool ACT>
 __global__ void __launch_bounds__(256)
@@ -1354,18 +1341,34 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 __global__ void reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
                               const uint16_t* __restrict__ bias,
                               uint16_t* __restrict__ y, int64_t ldy,
-                              const uint16_t* __restrict__ res, int64_t ldres) {
-  const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+                              const uint16_t* __restrict__ res, int64_t ldres, bool vec) {
+  // eight consecutive outputs of one row per thread (N is a multiple of 16)
+  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   const size_t total = (size_t)M * N;
   if (o >= total) return;
-  float sum = 0.f;
-  for (int sidx = 0; sidx < splits; ++sidx) sum += part[(size_t)sidx * total + o];
+  f4 s0 = *(const f4*)(part + o), s1 = *(const f4*)(part + o + 4);
+  for (int sidx = 1; sidx < splits; ++sidx) {  // split order, as the planes were cut
+    s0 += *(const f4*)(part + (size_t)sidx * total + o);
+    s1 += *(const f4*)(part + (size_t)sidx * total + o + 4);
+  }
   const int m = (int)(o / N);
   const int n = (int)(o % N);
-  _Float16 out = (_Float16)sum;
-  if (bias != nullptr) out = out + as_h(bias[n]);
-  if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
-  y[(size_t)m * ldy + n] = h_bits(out);
+  uint16_t* dst = y + (size_t)m * ldy + n;
+  const uint16_t* rsrc = res != nullptr ? res + (size_t)m * ldres + n : nullptr;
+  u4 packed;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    _Float16 out = (_Float16)(e < 4 ? s0[e] : s1[e - 4]);
+    if (bias != nullptr) out = out + as_h(bias[n + e]);
+    if (rsrc != nullptr) out = out + as_h(rsrc[e]);
+    if (vec) {
+      const uint32_t h = h_bits(out);
+      packed[e / 2] = (e & 1) ? (packed[e / 2] | (h << 16)) : h;
+    } else {
+      dst[e] = h_bits(out);
+    }
+  }
+  if (vec) *(u4*)dst = packed;
 }
 
 // ---------------------------------------------------------------------------
@@ -1518,11 +1521,8 @@ static hipError_t launch_decode_cfg(const GroupArgs& g, const DecodePlan& p, flo
     return hipErrorInvalidValue;
   }
   if (err != hipSuccess || p.splits == 1) return err;
-  const size_t total = (size_t)a.M * a.N;
-  reduce_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(part, p.splits, a.M, a.N,
-                                                                     a.bias, a.y, a.ldy,
-                                                                     a.res, a.ldres);
-  return hipGetLastError();
+  return launch_reduce_planes(part, p.splits, a.M, a.N, a.bias, a.y, a.ldy, a.res, a.ldres,
+                              stream);
 }
 
 template <int MT, int WAVES, bool G128>
@@ -1672,6 +1672,16 @@ hipError_t launch_prefill(const GemmArgs& a, const PrefillPlan& plan, void* part
   if (plan.bm == 128 && plan.bn == 256) return launch_prefill32_tile<4, 2, 2>(a, plan.splits, part, stream);
   if (plan.bm == 128 && plan.bn == 128) return launch_prefill32_tile<4, 1, 4>(a, plan.splits, part, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_reduce_planes(const float* part, int splits, int M, int N, const uint16_t* bias,
+                                uint16_t* y, int64_t ldy, const uint16_t* res, int64_t ldres,
+                                hipStream_t stream) {
+  const size_t units = (size_t)M * N / 8;
+  const bool vec = ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && (ldy % 8 == 0);
+  reduce_kernel<<<(unsigned)((units + 255) / 256), 256, 0, stream>>>(part, splits, M, N, bias, y,
+                                                                     ldy, res, ldres, vec);
+  return hipGetLastError();
 }
 
 hipError_t launch_dequant(const uint32_t* pq, const uint32_t* pz, const uint16_t* ps,

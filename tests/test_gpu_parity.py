@@ -190,8 +190,13 @@ def test_act_order_13b(hip_device, kn):
 
 def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
     """Act-order calls gather x into the packed row order in the workspace
-    when it has room, else the kernels gather per workgroup: the two feed the
-    same values to the same sums, so the outputs are bit-identical."""
+    when it has room, else the kernels gather per workgroup.  Where both
+    routes run the same kernel (decode; prefill tiles below 256 columns) they
+    feed the same values to the same sums and the outputs are bit-identical.
+    At M=300 the gathered rows go to the LDS-streamed 64 x 256 tile kernel,
+    whose two waves per column quarter sum alternate k halves and add them at
+    the end; the per-workgroup gather stays on the sequential-k kernel, so
+    there both are held to the oracle's tolerance instead."""
     k, n = 5120, 2048
     lay, w = oracle_w(k, n, 128, 4242, False, True)
     q4 = build(lay, hip_device)
@@ -218,8 +223,11 @@ def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
             if with_ws:  # the arrival-counter head stays zero for later split calls
                 assert not ws[:4096 * 4].any(), f"counter head written M={m}"
             outs.append(y.cpu())
-        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={m}"
         ref = gptq.gemm_ref(x.numpy(), w)
+        if m <= 64:
+            assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"M={m}"
+        else:
+            check_tol(outs[1], ref, f"in-kernel gather M={m} path {path}")
         check_tol(outs[0], ref, f"gather-first M={m} path {path}")
         if path == _lib.DW4_PATH_PREFILL:  # automatic split: gathered rows after the planes
             say(f"act-order gather-first after split-K planes M={m}")
@@ -273,7 +281,7 @@ def test_prefill_large_m_and_split_k(hip_device):
 @pytest.mark.parametrize("kn", SHAPES_7B, ids=lambda kn: f"{kn[0]}x{kn[1]}")
 def test_prefill_7b_large_m(hip_device, kn):
     """Config 3 at M = 1024 and 2048 on every 7B shape through the automatic
-    path (128-row tiles above M = 512)."""
+    path (128 x 128 or 128 x 256 tiles of the LDS-streamed kernel)."""
     k, n = kn
     lay, w = oracle_w(k, n, 128, 1000 + SHAPES_7B.index(kn), False, False)
     q4 = build(lay, hip_device)
@@ -286,12 +294,19 @@ def test_prefill_7b_large_m(hip_device, kn):
 
 
 @pytest.mark.parametrize("k,n,m,g,act", [(1024, 400, 600, 128, False), (2048, 4112, 1000, 128, False),
-                                         (1024, 400, 700, 64, True), (1024, 272, 520, 32, True)],
+                                         (1024, 400, 700, 64, True), (1024, 272, 520, 32, True),
+                                         (1024, 400, 300, 64, True), (1024, 272, 200, 32, False),
+                                         (1024, 4112, 2000, 32, True), (2048, 4112, 2000, 64, False)],
                          ids=["1024x400_M600", "2048x4112_M1000", "1024x400_M700_g64_act",
-                              "1024x272_M520_g32_act"])
+                              "1024x272_M520_g32_act", "1024x400_M300_g64_act",
+                              "1024x272_M200_g32", "1024x4112_M2000_g32_act",
+                              "2048x4112_M2000_g64"])
 def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
-    """128-row tiles (M > 512) with a partial last row tile and a partial
-    last column tile (N not a multiple of the 128/256-column tile)."""
+    """The LDS-streamed kernel's three tile shapes -- 64 x 256 (M = 200,
+    300), 128 x 128 (M = 520 .. 1000), 128 x 256 (M = 2000, where it needs
+    fewer rounds of workgroups) -- with a partial last row tile, a partial
+    last column tile (N not a multiple of the tile width) and group sizes
+    32 / 64 / 128, unsplit and split along K."""
     lay, w = oracle_w(k, n, g, 5000 + m, False, act)
     q4 = build(lay, hip_device)
     for split in (0, 1, 2):
