@@ -90,17 +90,22 @@ struct DecodePlan {
 };
 constexpr int kDecodeRegMinM = DW4_DECODE_REG_MIN_M;
 
-// LDS bytes a decode workgroup needs for a K range of `cps` chunks: each of
-// its waves stages the activation rows and metadata records of its own
-// ceil(cps / waves) chunks; the reduction reuses the space afterwards.
-inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
-  const size_t per_wave = (size_t)((cps + waves - 1) / waves);
-  const size_t rec = (size_t)(gs < kChunkK ? kChunkK / gs : 1) * kMetaBytes;
-  const size_t staged = (size_t)waves * per_wave * ((size_t)m * (kChunkK + 8) * 2 + rec);
-  const size_t mt = (size_t)((m + 15) / 16);
-  const size_t red = (size_t)waves * mt * 64 * 16;
-  const size_t b = staged > red ? staged : red;
+// LDS bytes of a decode workgroup's staging regions: each of its waves
+// stages the activation rows (kChunkK + 8 halfs per row) and the metadata
+// records (rec dwords per chunk) of its own per_wave chunks; 16-aligned.
+__host__ __device__ inline size_t decode_staged_bytes(int m, int per_wave, int rec, int waves) {
+  const size_t b = (size_t)waves * per_wave * ((size_t)m * (kChunkK + 8) * 2 + (size_t)rec * 4);
   return (b + 15) & ~(size_t)15;
+}
+
+// LDS bytes a decode workgroup needs for a K range of `cps` chunks: the
+// staging regions of ceil(cps / waves) chunks per wave, then the cross-wave
+// reduction's own region (so the reduction needs no barrier ahead of it).
+inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
+  const int per_wave = (cps + waves - 1) / waves;
+  const int rec = (gs < kChunkK ? kChunkK / gs : 1) * kMetaWords;
+  const size_t mt = (size_t)((m + 15) / 16);
+  return decode_staged_bytes(m, per_wave, rec, waves) + (size_t)waves * mt * 64 * 16;
 }
 
 // Waves per workgroup: enough to fill the chip with the strips available

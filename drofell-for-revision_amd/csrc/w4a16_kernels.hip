@@ -116,7 +116,8 @@ __device__ __forceinline__ uint32_t meta_word(const uint32_t* __restrict__ ps32,
 // contiguous per wave instruction); each word is dequantised in registers
 // straight into the B operand of v_mfma_f32_16x16x32_f16 (exact q - z in
 // fp16); the scale is applied per group in fp32; the waves' partial sums
-// meet in LDS in a fixed order at the end (deterministic).
+// meet in their own LDS region (one barrier) in a fixed order at the end
+// (deterministic).
 // ---------------------------------------------------------------------------
 constexpr int kXBatch = 8;  // activation units per lane per staging batch
 constexpr int kMBatch = 4;  // metadata dwords per lane per staging batch
@@ -168,7 +169,8 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   const int xupc = M * 16;  // 16-byte activation units per chunk
   const int xunits = nch * xupc;
   // group size >= 128: a chunk's scale and zero words travel with its
-  // weights in the ring (no staging); smaller groups stage their records
+  // weights in the ring (staging them costs an LDS round trip ahead of the
+  // first MFMA); smaller groups stage their records
   const int munits = G128 ? 0 : nch * rec;
   // Unit u = ((i * M + m) * 16 + q): 16-byte piece q of row m of the wave's
   // i-th chunk.  i = (u >> 4) / M by the host's multiplier (no division in
@@ -342,13 +344,13 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
     if (i < nch) chunk(qb[u], sb[u], zb[u], i);
   }
 
-  __syncthreads();  // staged activations are dead; reuse LDS for the reduction
-  f4* red = reinterpret_cast<f4*>(smem);
+  // the reduction region follows the staging regions
+  f4* red = reinterpret_cast<f4*>(smem + decode_staged_bytes(M, nch_max, rec, WAVES));
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) red[(wave * MT + mt) * 64 + lane] = tot[mt];
   __syncthreads();
 
-  const float* redf = reinterpret_cast<const float*>(smem);
+  const float* redf = reinterpret_cast<const float*>(red);
   const bool direct = gridDim.y == 1;
   for (int idx = tid; idx < MT * 256; idx += T) {
     const int llo = idx & 15;
