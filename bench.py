@@ -204,7 +204,11 @@ def crossover(mats, dev, steps: int, ms_list=(64, 128, 256, 512, 768, 1024, 2048
     """Per M: the 56-matrix pass through the native W4A16 kernel, through the
     reference's dense route (bit-exact dequantisation into one shared fp16
     buffer, then a library GEMM per matrix) and through a dense GEMM over an
-    already-reconstructed weight (the PEFT route that keeps the weight)."""
+    already-reconstructed weight.  For training with a kept weight (PEFT),
+    also forward plus activation gradient: packed (the native forward, then
+    ``transpose_matmul``, which runs the packed transposed kernel up to its
+    row limit) against dense (dequantise once, then a library GEMM for the
+    forward and one for the gradient over that weight)."""
     import torch
 
     kmax = max(k * n for _, k, n, _ in mats)
@@ -237,13 +241,32 @@ def crossover(mats, dev, steps: int, ms_list=(64, 128, 256, 512, 768, 1024, 2048
             for _, k, n, q4 in mats:
                 torch.matmul(xs[k], kept[(k, n)], out=ys[n])
 
+        gs_ = {n: torch.randn(m, n, device=dev, generator=gen).to(torch.float16)
+               for n in sorted({n for _, n in shapes})}
+        gx = {k: torch.empty(m, k, dtype=torch.float16, device=dev)
+              for k in sorted({k for k, _ in shapes})}
+
+        def peft_packed():
+            for _, k, n, q4 in mats:
+                q4.matmul(xs[k], output=ys[n])
+                q4.transpose_matmul(gs_[n], output=gx[k])
+
+        def peft_dense():
+            for _, k, n, q4 in mats:
+                w = temp[: k * n].view(k, n)
+                q4.get_float16_weights_matrix_v2(w)
+                torch.matmul(xs[k], w, out=ys[n])
+                torch.matmul(gs_[n], w.t(), out=gx[k])
+
         st = max(3, steps // 10)
         rec = {"m": m, "native_ms": round(time_callable(native, st, 2, dev), 4),
                "dense_ms": round(time_callable(dense, st, 2, dev), 4),
-               "dense_kept_weight_ms": round(time_callable(dense_kept, st, 2, dev), 4)}
+               "dense_kept_weight_ms": round(time_callable(dense_kept, st, 2, dev), 4),
+               "peft_packed_ms": round(time_callable(peft_packed, st, 2, dev), 4),
+               "peft_dense_ms": round(time_callable(peft_dense, st, 2, dev), 4)}
         log(json.dumps({"crossover": rec}))
         rows.append(rec)
-        del xs, ys
+        del xs, ys, gs_, gx
         torch.cuda.empty_cache()
     return rows
 

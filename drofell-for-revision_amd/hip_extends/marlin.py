@@ -45,12 +45,20 @@ class MarlinTuningParams:
     weight; ``grad_reconstruct_threshold`` serves PEFT that keeps the
     reconstructed weight for its backward (the forward then costs only the
     library GEMM).  ``None`` keeps that case on the packed kernel at every
-    size.  The defaults are MI355X crossovers measured over the Llama-2-7B
-    projections (``bench.py --crossover``), not the reference's RTX 3090 ones.
+    size.  The defaults are MI355X crossovers measured over the 56 Llama-2-7B
+    projections of the bench (``bench.py --crossover``, ms per pass), not the
+    reference's RTX 3090 ones:
+
+    * no kept weight, packed / dequantise + GEMM: M=2048 7.12 / 9.21,
+      M=4096 14.32 / 12.86, M=8192 28.49 / 23.59 -> dense from 4096 tokens;
+    * kept weight, forward + activation gradient, packed / dense: M=512
+      6.32 / 6.44, M=768 8.23 / 7.61, M=1024 9.20 / 8.57, M=2048
+      14.64 / 15.19, M=4096 26.80 / 23.15 -> dense from 768 tokens (4% slower
+      at 2048, 7-16% faster at every other size measured above it).
     """
 
-    reconstruct_threshold: Optional[int] = None
-    grad_reconstruct_threshold: Optional[int] = None
+    reconstruct_threshold: Optional[int] = 4096
+    grad_reconstruct_threshold: Optional[int] = 768
     reuse_reconstruct_cache_when_grad: Optional[bool] = None
 
     def __post_init__(self) -> None:

@@ -78,6 +78,36 @@ def test_marlin_linear_direct_and_dense(hip_device):
         lin.post_init(MarlinTuningParams(), cache)
 
 
+def test_marlin_kept_weight_crossover(hip_device):
+    """Training with a grad-tracking input keeps the reconstructed weight
+    from the default crossover on (dense forward, dense activation
+    gradient); one row below it the packed forward and the reconstruct-then-
+    dense gradient run.  Both sides match the fp64 reference."""
+    k, n = 1024, 2048
+    lay = make_layer(k, n, 128, seed=21, symmetric=True)
+    w = _w(lay)
+    maker = MarlinQuantLinearMaker(quantization_group_size=128, use_act_order=False)
+    with torch.device(hip_device):
+        lin = maker.make_linear(k, n, bias=False)
+    _load(lin, lay)
+    cache = MarlinDenseCache(hip_device)
+    maker.post_init(MarlinTuningParams(), cache)
+    cache.init_cache()
+    at = MarlinTuningParams().grad_reconstruct_threshold
+    assert at is not None
+    for m in (at - 1, at):
+        say(f"marlin kept-weight forward + gradient M={m} (default crossover {at})")
+        assert lin.q4_matrix.use_reconstructed_forward(m, cache_weight=True) == (m >= at)
+        xg = make_x(m, k, seed=300 + m).to(hip_device).requires_grad_(True)
+        y = lin(xg)
+        gout = make_x(m, n, seed=400 + m)
+        y.backward(gout.to(hip_device))
+        torch.cuda.synchronize()
+        check_tol(y.detach(), gptq.gemm_ref(xg.detach().cpu().numpy(), w), f"forward M={m}")
+        check_tol(xg.grad, gout.numpy().astype(np.float64) @ w.astype(np.float64).T,
+                  f"grad M={m}")
+
+
 def test_marlin_rejects_asymmetric_zeros(hip_device):
     lay = make_layer(256, 256, 128, seed=3, symmetric=False)
     maker = MarlinQuantLinearMaker(quantization_group_size=128, use_act_order=False)
