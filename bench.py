@@ -120,6 +120,20 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None, per_repl
     return ms, wall, sel
 
 
+DECODE_SOURCES = ("w4a16_kernels.hip", "w4a16_internal.h", "w4a16_device.h")
+
+
+def decode_source_sha256() -> str:
+    """Digest of the sources the decode kernel is built from."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in DECODE_SOURCES:
+        with open(os.path.join(REPO, "drofell-for-revision_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def time_callable(fn, steps: int, warmup: int, dev) -> float:
     """ms per call of `fn` (enqueues device work only), captured once into a
     HIP graph and replayed `steps` times between HIP events."""
@@ -690,10 +704,18 @@ def main() -> int:
         },
     }
 
+    # Measured HBM bytes per launch (two calibrated rocprofv3 counter passes),
+    # used only while the decode kernel's sources are the ones it was
+    # measured on.
     traffic_file = os.path.join(REPO, "profiles", "decode_traffic.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
-            result["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+            rec = json.load(f)
+        if rec.get("source_sha256") == decode_source_sha256():
+            result["roofline"]["traffic"] = rec.get("hbm_bytes_per_launch")
+        else:
+            result["roofline"]["traffic_note"] = ("profiles/decode_traffic.json was measured on "
+                                                  "other decode kernel sources")
 
     if not args.no_prefill:
         m = args.prefill_m
