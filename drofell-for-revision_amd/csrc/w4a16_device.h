@@ -58,6 +58,16 @@ __device__ __forceinline__ void zero_consts(uint32_t zword, int zshift, h2& nz10
   nz64 = as_h2((0xD400u | (ze << 4)) * 0x00010001u);
 }
 
+// Wait until every vector memory operation this wave has issued has
+// completed (s_waitcnt vmcnt(0), the other counters left alone).  Before a
+// workgroup barrier that precedes one thread's agent-scope release, it makes
+// each wave's own write-through stores visible at agent scope first: a
+// release orders only the issuing wave's operations, and the barrier itself
+// does not wait for memory.
+__device__ __forceinline__ void wait_own_stores() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+}
+
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

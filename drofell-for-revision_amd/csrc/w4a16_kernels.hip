@@ -969,8 +969,10 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   // cost several microseconds).  Layout per split plane (mtiles*ntiles*BM*BN
   // floats): [tile][mt*S + si][element e of the lane's float4][256 threads],
   // so each store instruction covers 256 contiguous bytes per wave.
-  // Ordering is the usual publish/consume pattern: the barrier orders every
-  // wave's stores before thread 0's release and counter increment; the last
+  // Ordering is the usual publish/consume pattern: every wave waits for its
+  // own stores to complete, the barrier then orders all of them before
+  // thread 0's release and counter increment (a release covers only the
+  // issuing wave's operations, and s_barrier does not wait for memory); the last
   // arriver's acquire (then the barrier) orders the other splits' partials
   // before its loads.  Fences run once per workgroup.
   const int tile_id = mtile * ntiles + ntile;
@@ -984,6 +986,7 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       for (int e = 0; e < 4; ++e)
         __hip_atomic_store(&part[(size_t)split * plane + tbase + (mt * S + si) * 1024 + e * 256],
                            acc[mt][si][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_own_stores();
   __shared__ int last_arrival;
   __syncthreads();
   if (tid == 0) {
@@ -1299,6 +1302,7 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       for (int i = 0; i < 16; ++i)
         __hip_atomic_store(&part[(size_t)split * plane + tbase + ((mt * P + p) * 16 + i) * 256],
                            acc[mt][p][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_own_stores();
   __shared__ int last_arrival;
   __syncthreads();
   if (tid == 0) {
