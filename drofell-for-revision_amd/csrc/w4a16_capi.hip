@@ -310,7 +310,13 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
   };
 
   if (decode) {
-    const dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
+    dw4::DecodePlan plan = dw4::plan_decode(m, k, n, group_size, cu_count());
+    // the register-fed kernel's K split is optional: without room (or
+    // alignment) for its planes the call runs unsplit
+    if (plan.reg && plan.splits > 1 &&
+        (workspace == nullptr || !aligned16(workspace) ||
+         workspace_bytes < dw4::split_ws_bytes(plan.splits, (size_t)m * n)))
+      plan = dw4::plan_decode(m, k, n, group_size, cu_count(), false);
     float* part = nullptr;
     size_t need = 0;
     if (plan.splits > 1) {
@@ -712,8 +718,9 @@ int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, i
   const int st = check_x(x, ldx, items[0].k);
   if (st != DW4_OK) return st;
   const int cus = cu_count();
-  if (m <= dw4::kDecodeMaxM && dw4::auto_decode(m, n_total, cus)) {
-    const dw4::DecodePlan plan = dw4::plan_decode(m, items[0].k, n_total, items[0].group_size, cus);
+  if (m <= dw4::kGroupDecodeMaxM && dw4::auto_decode(m, n_total, cus)) {
+    const dw4::DecodePlan plan =
+        dw4::plan_decode(m, items[0].k, n_total, items[0].group_size, cus, false);
     if (plan.splits == 1) {
       dw4::GroupArgs g{};
       g.count = count;

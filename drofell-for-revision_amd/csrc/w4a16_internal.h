@@ -14,8 +14,9 @@ namespace dw4 {
 constexpr int kChunkK = 128;  // sorted rows per packed chunk
 constexpr int kStripN = 16;   // columns per strip
 constexpr int kDecodeMaxM = 64;      // four 16-row MFMA tiles
-constexpr int kDecodeAutoMaxM = 24;        // DW4_PATH_AUTO picks decode up to this M,
-constexpr int kDecodeAutoMaxMNarrow = 32;  // and up to this M when strips <= CUs
+constexpr int kDecodeAutoMaxM = 48;        // DW4_PATH_AUTO picks decode up to this M,
+constexpr int kDecodeAutoMaxMNarrow = 64;  // and up to this M when strips <= CUs
+constexpr int kGroupDecodeMaxM = 32;       // grouped decode launches: two row tiles
 constexpr int kMetaBytes = 40;  // one (strip, group) scales+zeros record
 constexpr int kMetaWords = kMetaBytes / 4;
 #ifndef DW4_DECODE_UMAX
@@ -108,22 +109,55 @@ inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
   return decode_staged_bytes(m, per_wave, rec, waves) + (size_t)waves * mt * 64 * 16;
 }
 
+// Register-fed launch time model (microseconds), fitted to graph-replayed
+// times of the Llama-2-7B shapes at M = 8..64 on a 256-CU MI355X: every
+// round of workgroups costs the activation bytes one workgroup reads
+// (~33 GB/s per CU) plus its weight bytes (~27 GB/s per CU); a K split adds
+// the fp32 planes and the reduce launch.
+inline double decode_reg_cost(int m, int kc, int strips, int ss, int splits, int cus) {
+  const int cps = (kc + splits - 1) / splits;
+  const int real = (kc + cps - 1) / cps;
+  const int wgs = (strips + ss - 1) / ss * real;
+  const int rounds = (wgs + cus - 1) / cus;
+  const double a_mb = (double)m * cps * kChunkK * 2 / 1e6;
+  const double w_mb = (double)ss * cps * 1024 / 1e6;
+  return rounds * (29.9 * a_mb + 36.6 * w_mb) + (real > 1 ? 3.7 + 1.3 * (real - 1) : 0.0);
+}
+
 // Waves per workgroup: enough to fill the chip with the strips available
 // (one workgroup per 16-column strip), fewer for larger M whose activation
 // slices are bigger.  K is split across workgroups only where the staged
 // activations would not fit the LDS share of one workgroup (the CU's LDS
-// divided by the workgroups it is expected to hold).
-inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus) {
+// divided by the workgroups it is expected to hold).  The register-fed form
+// (5 <= M <= 64) takes the strips per workgroup (1, 2, 4) and K split (1, 2,
+// 4, 8) of least modelled time; grouped launches (single == false) keep one
+// or two strips and no split.
+inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus, bool single = true) {
   const int kc = k / kChunkK;
   const int strips = n / kStripN;
   if (m >= kDecodeRegMinM && m <= kDecodeMaxM) {
-    // register-fed: never split; two strips per workgroup share the A
-    // fragments when that still leaves a workgroup per CU; 16 waves for a
-    // single 16-row tile when there are no more workgroups than CUs
     DecodePlan r{1, kc, 8, 0};
     r.reg = true;
     r.ss = (strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
-    if (m <= 16 && r.ss == 1 && strips <= cus && kc >= 32) r.waves = 16;
+    if (single) {
+      const int mt = (m + 15) / 16;
+      const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
+      double best = decode_reg_cost(m, kc, strips, r.ss, 1, cus);
+      const int sss[3] = {1, 2, 4};
+      for (int ss : sss) {
+        if (ss == 4 && mt >= 3 && gpc > 1) continue;  // not instantiated
+        for (int sp = 1; sp <= 8 && sp * 8 <= kc; sp *= 2) {
+          const double c = decode_reg_cost(m, kc, strips, ss, sp, cus);
+          if (c < best) {
+            best = c;
+            r.ss = ss;
+            r.cps = (kc + sp - 1) / sp;
+            r.splits = (kc + r.cps - 1) / r.cps;
+          }
+        }
+      }
+    }
+    if (m <= 16 && r.ss == 1 && r.splits == 1 && strips <= cus && kc >= 32) r.waves = 16;
     r.smem = (size_t)r.waves * r.ss * ((m + 15) / 16) * 64 * 16;
     return r;
   }
@@ -176,7 +210,8 @@ inline size_t gather_bytes(int m, int k) { return ((size_t)m * k * 2 + 255) & ~(
 // split-K area: 256-aligned and past the arrival-counter head (declared
 // below), which must stay zero between calls.
 inline size_t gather_offset(size_t split);
-hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
+hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, float* part,
+                             hipStream_t stream);
 // One launch over every strip of g's matrices (decode plan with one split).
 hipError_t launch_decode_group(const GroupArgs& g, const DecodePlan& p, hipStream_t stream);
 // h[m, n] = fp16(silu(fp16(x @ W0 + b0)) * fp16(x @ W1 + b1)) for two matrices of equal N

@@ -383,7 +383,11 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
 // several rounds.  Here each wave loads its A fragments (16 bytes per lane
 // per 32-row k-step, from L2) into the same register ring as the weights,
 // and SS adjacent strips share them, so no LDS is needed until the final
-// cross-wave reduction and K is never split.
+// cross-wave reduction.  Every workgroup reads the A fragments of its whole
+// K range, so L2 -> CU activation traffic is (strips / SS) * M * K * 2
+// bytes: wider workgroups (SS = 4) with K split over gridDim.y workgroups
+// (fp32 planes summed in split order by reduce_kernel) keep that traffic
+// down where M * K is large, with the grid still filling the CUs.
 // Pair mode (SS = 2): workgroup s holds strip s of item 0 (gate) and of item 1
 // (up), which share perm, and writes fp16(silu(gate) * up) to item 0's
 // output; the two products never reach memory.
@@ -396,7 +400,7 @@ constexpr int kRegSingle = 0, kRegGroup = 1, kRegPair = 2;
 template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d, int K,
-                  int gs, int G) {
+                  int gs, int G, int cps, float* __restrict__ part) {
   constexpr bool PAIR = MODE == kRegPair;
   static_assert(!PAIR || SS == 2, "a pair workgroup holds one strip of each matrix");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -412,7 +416,10 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   const int j = lane & 15;
   const int kq = lane >> 4;
   const int KC = K / kChunkK;
-  const int nch = wave < KC ? (KC - wave + WAVES - 1) / WAVES : 0;
+  const int split = blockIdx.y;
+  const int c_begin = split * cps;
+  const int nc = min(KC, c_begin + cps) - c_begin;  // chunks of this split
+  const int nch = wave < nc ? (nc - wave + WAVES - 1) / WAVES : 0;
   // A rows: lanes past the last row read row M-1 (never stored)
   const _Float16* xr[MT];
 #pragma unroll
@@ -435,8 +442,9 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   u4 qb[U][SS];
   h8 ab[U][MT][4];
   uint32_t sb[U][SS][GPC], zb[U][SS][GPC];
+  const int c0 = __builtin_amdgcn_readfirstlane(c_begin + wave);  // this wave's first chunk
   auto load = [&](int slot_u, int i) {
-    const int c = wave + i * WAVES;
+    const int c = c0 + i * WAVES;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -546,6 +554,7 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
     const int64_t ldy = pick(d.ldy, item);
     const uint16_t* __restrict__ res = pick(d.res, item);
     const int64_t ldres = pick(d.ldres, item);
+    const int N = NS * kStripN;
     for (int idx = tid; idx < SS * MT * 256; idx += T) {
       const int sm = idx >> 8;  // ss * MT + mt
       const int ss = sm / MT;
@@ -558,6 +567,10 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
       if (m >= M || st >= NS) continue;
       const int L = lhi * 16 + llo;
       const int n = st * kStripN + llo;
+      if (MODE == kRegSingle && gridDim.y > 1) {  // this split's fp32 plane
+        part[((size_t)split * M + m) * N + n] = wave_sum(sm, L, r);
+        continue;
+      }
       _Float16 out = (_Float16)wave_sum(sm, L, r);
       if (bias != nullptr) out = out + as_h(bias[n]);
       if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
@@ -589,96 +602,146 @@ static Items make_items(const GroupArgs& g, int ss) {
   return d;
 }
 
+// K split of a register-fed launch: `splits` workgroups per strip group, each
+// over `cps` chunks, partial sums in fp32 planes `part` ([split][M][N]).
+struct RegSplit {
+  int splits = 1;
+  int cps = 0;
+  float* part = nullptr;
+};
+
 template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
-static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, hipStream_t stream) {
+static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, const RegSplit& sp,
+                                        hipStream_t stream) {
   const GemmArgs& a = g.a[0];
-  const dim3 grid((unsigned)(MODE == kRegPair ? a.N / kStripN : d.wg0[d.count]));
+  const dim3 grid((unsigned)(MODE == kRegPair ? a.N / kStripN : d.wg0[d.count]),
+                  (unsigned)sp.splits);
   const size_t smem = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
+  if (smem > 64 * 1024) {
+    static std::atomic<uint64_t> allowed{0};
+    const hipError_t e = allow_lds(reinterpret_cast<const void*>(
+                                       &decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT, MODE>),
+                                   smem, allowed);
+    if (e != hipSuccess) return e;
+  }
   decode_reg_kernel<MT, WAVES, U, SS, GPC, ACT, MODE><<<grid, WAVES * 64, smem, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, d, a.K, a.gs, a.G);
-  return hipGetLastError();
+      (const _Float16*)a.x, a.ldx, a.M, d, a.K, a.gs, a.G, sp.cps, sp.part);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess || sp.splits == 1) return e;
+  return launch_reduce_planes(sp.part, sp.splits, a.M, a.N, a.bias, a.y, a.ldy, a.res, a.ldres,
+                              stream);
 }
 
 // Deepest ring (chunks in flight per wave) that a variant holds without
 // spilling.  The A fragments of one chunk take 16 * MT registers per lane
-// (their act-order gathers more while in flight); 16-wave workgroups have
-// 128 registers per lane, 8-wave ones 256.
-constexpr int decode_reg_umax(int mt, int waves, int gpc, bool act) {
+// (their act-order gathers more while in flight) and each strip's weight
+// words 4 more; 16-wave workgroups have 128 registers per lane, 8-wave ones
+// 256.
+constexpr int decode_reg_umax(int mt, int waves, int ss, int gpc, bool act) {
   return waves == 16 ? ((act || gpc == 4) ? 2 : 4)
+         : ss == 4   ? (mt == 1 ? (gpc == 4 ? 2 : 4) : (mt == 2 ? 2 : 1))
          : mt == 1   ? 4
          : act       ? 1
                      : (mt == 2 ? 2 : 1);
 }
 
-// Ring depth U: the deepest allowed, at most the chunks of the shortest wave.
+// Ring depth U: the deepest allowed, at most the chunks of the shortest wave
+// (of the shortest split).
 template <int MT, int WAVES, int SS, int GPC, bool ACT, int MODE>
-static hipError_t launch_decode_reg_u(const GroupArgs& g, const Items& d, hipStream_t stream) {
-  const int per_wave = (g.a[0].K / kChunkK) / WAVES;
-  constexpr int umax = decode_reg_umax(MT, WAVES, GPC, ACT);
+static hipError_t launch_decode_reg_u(const GroupArgs& g, const Items& d, const RegSplit& sp,
+                                      hipStream_t stream) {
+  const int kc = g.a[0].K / kChunkK;
+  const int shortest = sp.splits > 1 ? kc - (sp.splits - 1) * sp.cps : kc;
+  const int per_wave = shortest / WAVES;
+  constexpr int umax = decode_reg_umax(MT, WAVES, SS, GPC, ACT);
   if constexpr (umax >= 4) {
-    if (per_wave >= 4) return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT, MODE>(g, d, stream);
+    if (per_wave >= 4)
+      return launch_decode_reg_cfg<MT, WAVES, 4, SS, GPC, ACT, MODE>(g, d, sp, stream);
   }
   if constexpr (umax >= 2) {
-    if (per_wave >= 2) return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT, MODE>(g, d, stream);
+    if (per_wave >= 2)
+      return launch_decode_reg_cfg<MT, WAVES, 2, SS, GPC, ACT, MODE>(g, d, sp, stream);
   }
   // 16 waves are planned only where every wave gets two chunks or more
   if constexpr (WAVES == 16) return hipErrorInvalidValue;
-  else return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT, MODE>(g, d, stream);
+  else return launch_decode_reg_cfg<MT, WAVES, 1, SS, GPC, ACT, MODE>(g, d, sp, stream);
 }
 
 template <int MT, int WAVES, int SS, bool ACT, int MODE>
-static hipError_t launch_decode_reg_g(const GroupArgs& g, const Items& d, hipStream_t stream) {
+static hipError_t launch_decode_reg_g(const GroupArgs& g, const Items& d, const RegSplit& sp,
+                                      hipStream_t stream) {
   const int gs = g.a[0].gs;
   const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
-  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, MODE>(g, d, stream);
-  if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, MODE>(g, d, stream);
-  return launch_decode_reg_u<MT, WAVES, SS, 4, ACT, MODE>(g, d, stream);
+  if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, MODE>(g, d, sp, stream);
+  // four strips of three or four row tiles hold one group per chunk only
+  // (more per-chunk scale and zero words do not fit the registers)
+  if constexpr (SS == 4 && MT >= 3) {
+    return hipErrorInvalidValue;
+  } else {
+    if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, MODE>(g, d, sp, stream);
+    return launch_decode_reg_u<MT, WAVES, SS, 4, ACT, MODE>(g, d, sp, stream);
+  }
 }
 
 template <int MT, int WAVES, int SS, int MODE>
-static hipError_t launch_decode_reg_w(const GroupArgs& g, hipStream_t stream) {
+static hipError_t launch_decode_reg_w(const GroupArgs& g, const RegSplit& sp, hipStream_t stream) {
   if (g.a[0].perm == nullptr) {
     const Items d = make_items(g, MODE == kRegPair ? 1 : SS);
-    return launch_decode_reg_g<MT, WAVES, SS, false, MODE>(g, d, stream);
+    return launch_decode_reg_g<MT, WAVES, SS, false, MODE>(g, d, sp, stream);
   }
-  // act-order gathers for four tiles and two strips do not fit the registers
-  if constexpr (MT == 4 && SS == 2 && MODE != kRegPair) {
+  // act-order gathers for four tiles and two strips, or four strips, do
+  // not fit the registers
+  if constexpr (MODE != kRegPair && ((MT == 4 && SS == 2) || SS == 4)) {
     const Items d = make_items(g, 1);
-    return launch_decode_reg_g<MT, WAVES, 1, true, MODE>(g, d, stream);
+    return launch_decode_reg_g<MT, WAVES, 1, true, MODE>(g, d, sp, stream);
   } else {
     const Items d = make_items(g, MODE == kRegPair ? 1 : SS);
-    return launch_decode_reg_g<MT, WAVES, SS, true, MODE>(g, d, stream);
+    return launch_decode_reg_g<MT, WAVES, SS, true, MODE>(g, d, sp, stream);
   }
 }
 
 template <int MT, int MODE>
-static hipError_t launch_decode_reg_mt(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
-  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2, MODE>(g, stream)
-                   : launch_decode_reg_w<MT, 8, 1, MODE>(g, stream);
+static hipError_t launch_decode_reg_mt(const GroupArgs& g, const DecodePlan& p,
+                                       const RegSplit& sp, hipStream_t stream) {
+  if (p.ss == 4) {
+    if constexpr (MODE == kRegSingle) return launch_decode_reg_w<MT, 8, 4, MODE>(g, sp, stream);
+    else return hipErrorInvalidValue;
+  }
+  return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2, MODE>(g, sp, stream)
+                   : launch_decode_reg_w<MT, 8, 1, MODE>(g, sp, stream);
 }
 
 // Grouped launches come from the automatic path, which takes decode only up
-// to M = 32 (two row tiles).
+// to M = 32 (two row tiles), and are never split.
 template <int MT>
-static hipError_t launch_decode_reg_m(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
-  if (g.count == 1) return launch_decode_reg_mt<MT, kRegSingle>(g, p, stream);
-  if constexpr (MT <= 2) return launch_decode_reg_mt<MT, kRegGroup>(g, p, stream);
+static hipError_t launch_decode_reg_m(const GroupArgs& g, const DecodePlan& p, const RegSplit& sp,
+                                      hipStream_t stream) {
+  if (g.count == 1) return launch_decode_reg_mt<MT, kRegSingle>(g, p, sp, stream);
+  if (sp.splits != 1) return hipErrorInvalidValue;
+  if constexpr (MT <= 2) return launch_decode_reg_mt<MT, kRegGroup>(g, p, sp, stream);
   else return hipErrorInvalidValue;
 }
 
-hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, hipStream_t stream) {
+hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, float* part,
+                             hipStream_t stream) {
   const int M = g.a[0].M;
+  RegSplit sp;
+  sp.splits = p.splits;
+  sp.cps = p.cps;
+  sp.part = part;
+  if (sp.splits > 1 && (part == nullptr || g.count != 1)) return hipErrorInvalidValue;
   if (M <= 16) {
-    if (p.waves == 16) {  // planner: ss == 1
-      return g.count == 1 ? launch_decode_reg_w<1, 16, 1, kRegSingle>(g, stream)
-                          : launch_decode_reg_w<1, 16, 1, kRegGroup>(g, stream);
+    if (p.waves == 16) {  // planner: ss == 1, unsplit
+      if (sp.splits != 1) return hipErrorInvalidValue;
+      return g.count == 1 ? launch_decode_reg_w<1, 16, 1, kRegSingle>(g, sp, stream)
+                          : launch_decode_reg_w<1, 16, 1, kRegGroup>(g, sp, stream);
     }
-    return launch_decode_reg_m<1>(g, p, stream);
+    return launch_decode_reg_m<1>(g, p, sp, stream);
   }
   if (p.waves != 8) return hipErrorInvalidValue;
-  if (M <= 32) return launch_decode_reg_m<2>(g, p, stream);
-  if (M <= 48) return launch_decode_reg_m<3>(g, p, stream);
-  if (M <= 64) return launch_decode_reg_m<4>(g, p, stream);
+  if (M <= 32) return launch_decode_reg_m<2>(g, p, sp, stream);
+  if (M <= 48) return launch_decode_reg_m<3>(g, p, sp, stream);
+  if (M <= 64) return launch_decode_reg_m<4>(g, p, sp, stream);
   return hipErrorInvalidValue;
 }
 
@@ -688,8 +751,9 @@ hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipS
   gp.a[0].y = h;  // the pair's output goes where item 0's would
   gp.a[0].ldy = ldh;
   const int M = g.a[0].M;
-  if (M <= 16) return launch_decode_reg_w<1, 8, 2, kRegPair>(gp, stream);
-  if (M <= kPairMaxM) return launch_decode_reg_w<2, 8, 2, kRegPair>(gp, stream);
+  const RegSplit sp{1, g.a[0].K / kChunkK, nullptr};
+  if (M <= 16) return launch_decode_reg_w<1, 8, 2, kRegPair>(gp, sp, stream);
+  if (M <= kPairMaxM) return launch_decode_reg_w<2, 8, 2, kRegPair>(gp, sp, stream);
   return hipErrorInvalidValue;
 }
 
@@ -1575,7 +1639,7 @@ static hipError_t launch_decode_mt(const GroupArgs& g, const DecodePlan& p, floa
 
 static hipError_t launch_decode_any(const GroupArgs& g, const DecodePlan& p, float* part,
                                     hipStream_t stream) {
-  if (p.reg) return launch_decode_reg(g, p, stream);
+  if (p.reg) return launch_decode_reg(g, p, part, stream);
   switch ((g.a[0].M + 15) / 16) {
     case 1: return launch_decode_mt<1>(g, p, part, stream);
     case 2: return launch_decode_mt<2>(g, p, part, stream);

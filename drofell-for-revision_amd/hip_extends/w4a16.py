@@ -39,8 +39,8 @@ from . import _lib
 class TuningParams:
     # Flattened M at or below which the register-dequant decode kernel runs
     # (at most 64: four 16-row MFMA tiles); above it the prefill kernel runs.
-    # None leaves the choice to the library: decode up to M = 24, or up to
-    # M = 32 when N / 16 is at most the device's CU count.
+    # None leaves the choice to the library: decode up to M = 48, or up to
+    # M = 64 when N / 16 is at most the device's CU count.
     DECODE_MAX_M: Optional[int] = None
     # Largest flattened M the shared workspace is sized for.  Larger calls
     # still run, with the prefill kernel unsplit along K.

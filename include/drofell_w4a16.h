@@ -116,7 +116,7 @@ enum {
 
 /* Path selection for dw4_gemm_path(). */
 enum {
-  DW4_PATH_AUTO = 0,     /* decode for M <= 24, or M <= 32 when N / 16 <= CUs */
+  DW4_PATH_AUTO = 0,     /* decode for M <= 48, or M <= 64 when N / 16 <= CUs */
   DW4_PATH_DECODE = 1,   /* register-dequant MFMA kernel, M <= 64 */
   DW4_PATH_PREFILL = 2   /* LDS-staged MFMA kernel, any M */
 };
@@ -135,7 +135,10 @@ int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
  * it returns 0).  With act_order it includes M*K fp16 for x gathered into
  * the packed row order (placed after the split-K area and the arrival
  * counters); a call whose workspace lacks that room gathers inside every
- * workgroup instead: the same result bit for bit, slower. */
+ * workgroup instead: the same result bit for bit, slower.  For 5 <= M <= 64
+ * the decode kernel may split K over workgroups (fp32 planes in the
+ * workspace); given less than this size it runs unsplit instead (a valid
+ * result, summed in another order). */
 int dw4_workspace_size(int m, int k, int n, int group_size, int act_order,
                        size_t* workspace_bytes);
 
@@ -256,10 +259,10 @@ typedef struct dw4_item {
 } dw4_item;
 
 /* y_i = x @ W_i (+ bias_i) for 1..4 matrices that share x, k and
- * group_size (with perm on all or on none).  Where DW4_PATH_AUTO would take
- * the decode kernel for the summed N, one launch covers every strip of every
- * matrix; otherwise (and where that launch would split K) the matrices run
- * one after another as dw4_gemm does.  workspace: at least
+ * group_size (with perm on all or on none).  For m <= 32 where
+ * DW4_PATH_AUTO would take the decode kernel for the summed N, one launch
+ * covers every strip of every matrix; otherwise the matrices run one after
+ * another as dw4_gemm does.  workspace: at least
  * dw4_workspace_size of each item. */
 int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, int64_t ldx,
                    void* workspace, size_t workspace_bytes, void* stream);

@@ -158,8 +158,14 @@ def test_make_perm_rejects_bad_g_idx():
 def test_workspace_size_rules():
     # M=1 activations fit the decode workgroup's LDS: one split, no workspace
     assert _lib.workspace_size(1, 4096, 4096, 128, False) == 0
-    # M = 5..64 runs the register-fed decode kernel: K is never split
-    assert _lib.workspace_size(16, 11008, 4096, 128, False) == 0
+    # M = 5..64 runs the register-fed decode kernel.  Wide N takes four
+    # strips per workgroup unsplit; long K splits over workgroups (fp32
+    # planes [splits][M][N] after the 16 KiB arrival-counter head) so that
+    # each workgroup reads less of x (256 CUs without a device)
+    head = 4096 * 4
+    assert _lib.workspace_size(16, 4096, 11008, 128, False) == 0
+    assert _lib.workspace_size(16, 11008, 4096, 128, False) == head + 2 * 16 * 4096 * 4
+    assert _lib.workspace_size(64, 11008, 4096, 128, False) == head + 4 * 64 * 4096 * 4
     # act-order gathers x into the packed row order first: M * K fp16
     # (rounded to 256 bytes) after the 16 KiB arrival-counter head, which
     # every call leaves zero for the split calls that share the buffer
@@ -173,13 +179,12 @@ def test_workspace_size_rules():
         (split + 255) // 256 * 256 + 256 * 4096 * 2
     # the per-matrix query covers every M up to max_m, gather included
     assert _lib.query_sizes(5120, 13824, 128, True, 64)["workspace"] >= 64 * 5120 * 2
-    # the automatic path takes decode up to M = 24, and up to M = 32 when
+    # the automatic path takes decode up to M = 48, and up to M = 64 when
     # N / 16 <= CUs (256 without a device); above, split-K prefill needs a
     # workspace at these shapes
-    assert _lib.workspace_size(24, 4096, 11008, 128, False) == 0
-    assert _lib.workspace_size(32, 4096, 11008, 128, False) > 0
-    assert _lib.workspace_size(32, 11008, 4096, 128, False) == 0
-    assert _lib.workspace_size(40, 11008, 4096, 128, False) > 0
+    assert _lib.workspace_size(48, 4096, 11008, 128, False) == 0
+    assert _lib.workspace_size(56, 4096, 11008, 128, False) > 0
+    assert _lib.workspace_size(48, 5120, 5120, 128, False) == head + 2 * 48 * 5120 * 4
     # M=4 x K=13824 does not fit the staged kernel's LDS share: fp32 split-K
     # planes.  A split call's workspace: a fixed 16 KiB head of arrival
     # counters, then whole fp32 partial planes [splits][M][N]

@@ -149,6 +149,42 @@ def test_decode_7b_shapes(hip_device, kn):
         check_tol(y, gptq.gemm_ref(x.numpy(), w), f"decode {k}x{n} M={m}")
 
 
+@pytest.mark.parametrize("k,n,m,g", [(11008, 4096, 16, 128), (11008, 4096, 40, 128),
+                                     (4096, 4096, 64, 128), (4096, 11008, 24, 128),
+                                     (2048, 8208, 16, 64), (8192, 2064, 24, 32),
+                                     (8192, 2064, 33, 128)],
+                         ids=["11008x4096_M16", "11008x4096_M40", "4096x4096_M64",
+                              "4096x11008_M24", "2048x8208_M16_g64", "8192x2064_M24_g32",
+                              "8192x2064_M33"])
+def test_decode_wide_and_split_plans(hip_device, k, n, m, g):
+    """The register-fed decode kernel with four strips per workgroup and K
+    split over workgroups (fp32 planes summed in split order), with a
+    partial last strip group (N / 16 not a multiple of 4) and groups of 32 /
+    64: within tolerance of the oracle, deterministic, and -- given no
+    workspace -- the unsplit plan, also within tolerance."""
+    lay, w = oracle_w(k, n, g, 7000 + m, False, False)
+    q4 = build(lay, hip_device)
+    lib = _lib.load()
+    x = make_x(m, k, seed=m + 31)
+    xd = x.to(hip_device)
+    ref = gptq.gemm_ref(x.numpy(), w)
+    outs = []
+    for size in (_lib.workspace_size(m, k, n, g, False),) * 2 + (0,):
+        say(f"decode wide/split {k}x{n} M={m} g={g} workspace={size}")
+        ws = torch.zeros(max(16, size), dtype=torch.uint8, device=hip_device)
+        y = torch.empty(m, n, dtype=torch.float16, device=hip_device)
+        st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, m, k, n, g, xd.data_ptr(), k,
+                               q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(),
+                               None, None, y.data_ptr(), n, ws.data_ptr(), size,
+                               torch.cuda.current_stream().cuda_stream)
+        assert st == _lib.DW4_OK, _lib.strerror(st)
+        torch.cuda.synchronize()
+        assert not ws[:4096 * 4].any()
+        check_tol(y, ref, f"decode {k}x{n} M={m} g={g} workspace {size}")
+        outs.append(y.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 @pytest.mark.parametrize("kn", SHAPES_7B, ids=lambda kn: f"{kn[0]}x{kn[1]}")
 def test_prefill_7b_shapes(hip_device, kn):
     k, n = kn
@@ -190,9 +226,12 @@ def test_act_order_13b(hip_device, kn):
 
 def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
     """Act-order calls gather x into the packed row order in the workspace
-    when it has room, else the kernels gather per workgroup.  Where both
-    routes run the same kernel (decode; prefill tiles below 256 columns) they
-    feed the same values to the same sums and the outputs are bit-identical.
+    when it has room, else the kernels gather per workgroup.  The second
+    route gets room for the decode plan's split-K planes but none for the
+    gathered rows, so both routes run the same plan.
+    Where that is the same kernel (decode; prefill tiles below 256 columns)
+    they feed the same values to the same sums and the outputs are
+    bit-identical.
     At M=300 the gathered rows go to the LDS-streamed 64 x 256 tile kernel,
     whose two waves per column quarter sum alternate k halves and add them at
     the end; the per-workgroup gather stays on the sequential-k kernel, so
@@ -208,15 +247,18 @@ def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
         xd = x.to(hip_device)
         outs = []
         for with_ws in (True, False):
-            ws = torch.zeros(_lib.workspace_size(m, k, n, 128, True) if with_ws else 0,
-                             dtype=torch.uint8, device=hip_device)
+            # without act-order room: the decode plan's split planes only (the
+            # prefill calls below are unsplit)
+            size = _lib.workspace_size(m, k, n, 128, True) if with_ws else \
+                (_lib.workspace_size(m, k, n, 128, False) if path == _lib.DW4_PATH_DECODE else 0)
+            ws = torch.zeros(max(16, size), dtype=torch.uint8, device=hip_device)
             if with_ws:
                 assert ws.numel() >= m * k * 2  # room for the gathered activations
             y = torch.empty(m, n, dtype=torch.float16, device=hip_device)
             st = lib.dw4_gemm_path(path, 1, m, k, n, 128, xd.data_ptr(), k,
                                    q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
                                    q4.scales.data_ptr(), q4.perm.data_ptr(), None,
-                                   y.data_ptr(), n, ws.data_ptr() if with_ws else None,
+                                   y.data_ptr(), n, ws.data_ptr(),
                                    ws.numel(), torch.cuda.current_stream().cuda_stream)
             assert st == _lib.DW4_OK, _lib.strerror(st)
             torch.cuda.synchronize()
