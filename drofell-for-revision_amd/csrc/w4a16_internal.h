@@ -109,19 +109,33 @@ inline size_t decode_smem_bytes(int m, int cps, int gs, int waves) {
   return decode_staged_bytes(m, per_wave, rec, waves) + (size_t)waves * mt * 64 * 16;
 }
 
+#ifndef DW4_REG_LDSX
+#define DW4_REG_LDSX 1
+#endif
+// Register-fed variants that load A as whole 128-byte lines and rearrange it
+// through LDS: all without act-order except those whose extra live
+// registers would spill (four strips beyond one row tile with 32- or 64-row
+// groups or four row tiles, two strips of four row tiles with small groups).
+constexpr bool decode_reg_lx(int mt, int ss, int gpc, bool act) {
+  return DW4_REG_LDSX && !act && !(ss == 4 && mt >= 2 && (gpc > 1 || mt == 4)) &&
+         !(mt == 4 && ss == 2 && gpc > 1);
+}
+
 // Register-fed launch time model (microseconds), fitted to graph-replayed
 // times of the Llama-2-7B shapes at M = 8..64 on a 256-CU MI355X: every
-// round of workgroups costs the activation bytes one workgroup reads
-// (~33 GB/s per CU) plus its weight bytes (~27 GB/s per CU); a K split adds
-// the fp32 planes and the reduce launch.
-inline double decode_reg_cost(int m, int kc, int strips, int ss, int splits, int cus) {
+// round of workgroups costs the activation bytes one workgroup reads (~66
+// GB/s per CU as whole lines, ~34 GB/s in operand order) plus its weight
+// bytes (~25 GB/s per CU); a K split adds the fp32 planes and the reduce
+// launch.
+inline double decode_reg_cost(int m, int kc, int strips, int ss, int splits, int gpc, int cus) {
   const int cps = (kc + splits - 1) / splits;
   const int real = (kc + cps - 1) / cps;
   const int wgs = (strips + ss - 1) / ss * real;
   const int rounds = (wgs + cus - 1) / cus;
   const double a_mb = (double)m * cps * kChunkK * 2 / 1e6;
   const double w_mb = (double)ss * cps * 1024 / 1e6;
-  return rounds * (29.9 * a_mb + 36.6 * w_mb) + (real > 1 ? 3.7 + 1.3 * (real - 1) : 0.0);
+  const double a_rate = decode_reg_lx((m + 15) / 16, ss, gpc, false) ? 15.2 : 29.3;
+  return rounds * (a_rate * a_mb + 40.3 * w_mb) + (real > 1 ? 3.0 + 1.4 * (real - 1) : 0.0);
 }
 
 // Waves per workgroup: enough to fill the chip with the strips available
@@ -142,12 +156,12 @@ inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus, bool single 
     if (single) {
       const int mt = (m + 15) / 16;
       const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
-      double best = decode_reg_cost(m, kc, strips, r.ss, 1, cus);
+      double best = decode_reg_cost(m, kc, strips, r.ss, 1, gpc, cus);
       const int sss[3] = {1, 2, 4};
       for (int ss : sss) {
         if (ss == 4 && mt >= 3 && gpc > 1) continue;  // not instantiated
         for (int sp = 1; sp <= 8 && sp * 8 <= kc; sp *= 2) {
-          const double c = decode_reg_cost(m, kc, strips, ss, sp, cus);
+          const double c = decode_reg_cost(m, kc, strips, ss, sp, gpc, cus);
           if (c < best) {
             best = c;
             r.ss = ss;

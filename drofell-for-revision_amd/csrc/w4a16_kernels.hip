@@ -397,6 +397,7 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
 // matrices, item looked up per workgroup) or kRegPair (gate/up, above).
 constexpr int kRegSingle = 0, kRegGroup = 1, kRegPair = 2;
 
+
 template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d, int K,
@@ -424,6 +425,30 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   const _Float16* xr[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xr[mt] = x + (size_t)min(mt * 16 + j, M - 1) * ldx;
+  // Without act-order the A fragments are loaded as whole 128-byte lines
+  // (8 lanes per row; load b of a 64-row half h holds rows 8b + lane / 8,
+  // k units 8h + lane % 8) -- half the L2 requests of loading them in the
+  // MFMA operand order, which gives each 16-lane row group half a line --
+  // and rearranged through this wave's own 4 KiB LDS region per row tile:
+  // unit (row r, k unit v) at r * 16 + (v ^ f(r)), f(r) = (r & 1) * 8 + r / 2,
+  // so the 16 rows of an operand read and the two rows of 8 lanes each of a
+  // store both hit 16 distinct 16-byte bank groups.
+  constexpr bool LX = decode_reg_lx(MT, SS, GPC, ACT);
+  uint32_t xl[MT][2];  // element offsets from x (M * ldx < 2^31)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      xl[mt][b] = (uint32_t)(min(mt * 16 + 8 * b + (lane >> 3), M - 1) * (int)ldx + 8 * (lane & 7));
+  auto swz = [](int r, int v) { return r * 16 + (v ^ (((r & 1) << 3) | (r >> 1))); };
+  const int wr_row = lane >> 3;  // + 8 b
+  uint32_t xoff_w[4], xoff_r[4];  // byte offsets in the wave's region, per load / k-step
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    xoff_w[t] = (uint32_t)swz(8 * (t & 1) + wr_row, 8 * (t >> 1) + (lane & 7)) * 16;
+    xoff_r[t] = (uint32_t)swz(j, 4 * t + kq) * 16;
+  }
+  unsigned char* xs = smem + (size_t)wave * MT * 4096;
 
   const u4* qp[SS];
   const uint32_t* sp[SS];
@@ -448,8 +473,12 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        ab[slot_u][mt][t] = load_x_unit<ACT>(xr[mt], perm, c * kChunkK + 32 * t + 8 * kq);
+      for (int t = 0; t < 4; ++t) {
+        if constexpr (LX)
+          ab[slot_u][mt][t] = *(const h8*)(x + xl[mt][t & 1] + (size_t)c * kChunkK + 64 * (t >> 1));
+        else
+          ab[slot_u][mt][t] = load_x_unit<ACT>(xr[mt], perm, c * kChunkK + 32 * t + 8 * kq);
+      }
 #pragma unroll
     for (int ss = 0; ss < SS; ++ss) {
       qb[slot_u][ss] = __builtin_nontemporal_load(qp[ss] + (size_t)c * 64);
@@ -468,6 +497,16 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
     for (int mt = 0; mt < MT; ++mt) tot[ss][mt] = f4{0.f, 0.f, 0.f, 0.f};
   const uint32_t magic = kMagic;
   auto consume = [&](int slot_u) {
+    if constexpr (LX) {  // the slot's registers go out in load order, come back in operand order
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) *(h8*)(xs + mt * 4096 + xoff_w[t]) = ab[slot_u][mt][t];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) ab[slot_u][mt][t] = *(const h8*)(xs + mt * 4096 + xoff_r[t]);
+    }
 #pragma unroll
     for (int ss = 0; ss < SS; ++ss)
 #pragma unroll
@@ -514,7 +553,9 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   for (int u = 0; u < U; ++u)
     if (i0 + U + u < nch) consume(u);
 
-  // fixed-order reduction across waves, then fp16 (+ bias) output
+  // fixed-order reduction across waves, then fp16 (+ bias) output (the
+  // reduction region overlaps other waves' A regions: all waves first)
+  if constexpr (LX) __syncthreads();
   f4* red = reinterpret_cast<f4*>(smem);
 #pragma unroll
   for (int ss = 0; ss < SS; ++ss)
@@ -616,7 +657,9 @@ static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, cons
   const GemmArgs& a = g.a[0];
   const dim3 grid((unsigned)(MODE == kRegPair ? a.N / kStripN : d.wg0[d.count]),
                   (unsigned)sp.splits);
-  const size_t smem = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
+  const size_t red_bytes = (size_t)WAVES * SS * MT * 64 * sizeof(f4);
+  const size_t xs_bytes = decode_reg_lx(MT, SS, GPC, ACT) ? (size_t)WAVES * MT * 4096 : 0;
+  const size_t smem = red_bytes > xs_bytes ? red_bytes : xs_bytes;
   if (smem > 64 * 1024) {
     static std::atomic<uint64_t> allowed{0};
     const hipError_t e = allow_lds(reinterpret_cast<const void*>(
@@ -638,7 +681,8 @@ static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, cons
 // words 4 more; 16-wave workgroups have 128 registers per lane, 8-wave ones
 // 256.
 constexpr int decode_reg_umax(int mt, int waves, int ss, int gpc, bool act) {
-  return waves == 16 ? ((act || gpc == 4) ? 2 : 4)
+  return waves == 16 ? ((act || gpc == 4 || decode_reg_lx(mt, ss, gpc, act)) ? 2 : 4)
+         : ss == 4 && mt == 1 && gpc == 2 ? 2
          : ss == 4   ? (mt == 1 ? (gpc == 4 ? 2 : 4) : (mt == 2 ? 2 : 1))
          : mt == 1   ? 4
          : act       ? 1

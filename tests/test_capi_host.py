@@ -164,8 +164,9 @@ def test_workspace_size_rules():
     # each workgroup reads less of x (256 CUs without a device)
     head = 4096 * 4
     assert _lib.workspace_size(16, 4096, 11008, 128, False) == 0
-    assert _lib.workspace_size(16, 11008, 4096, 128, False) == head + 2 * 16 * 4096 * 4
-    assert _lib.workspace_size(64, 11008, 4096, 128, False) == head + 4 * 64 * 4096 * 4
+    assert _lib.workspace_size(16, 11008, 4096, 128, False) == 0
+    assert _lib.workspace_size(32, 11008, 4096, 128, False) == head + 2 * 32 * 4096 * 4
+    assert _lib.workspace_size(48, 11008, 4096, 128, False) == head + 4 * 48 * 4096 * 4
     # act-order gathers x into the packed row order first: M * K fp16
     # (rounded to 256 bytes) after the 16 KiB arrival-counter head, which
     # every call leaves zero for the split calls that share the buffer
@@ -184,7 +185,7 @@ def test_workspace_size_rules():
     # workspace at these shapes
     assert _lib.workspace_size(48, 4096, 11008, 128, False) == 0
     assert _lib.workspace_size(56, 4096, 11008, 128, False) > 0
-    assert _lib.workspace_size(48, 5120, 5120, 128, False) == head + 2 * 48 * 5120 * 4
+    assert _lib.workspace_size(48, 5120, 5120, 128, False) == 0
     # M=4 x K=13824 does not fit the staged kernel's LDS share: fp32 split-K
     # planes.  A split call's workspace: a fixed 16 KiB head of arrival
     # counters, then whole fp32 partial planes [splits][M][N]
