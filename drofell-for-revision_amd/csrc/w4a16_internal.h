@@ -79,6 +79,7 @@ struct Items {
 // 32x32x16 MFMA kernel), column tile bn (128 or 256), split-K factor.
 struct PrefillPlan {
   int bm, bn, splits;
+  int waves = 8;  // LDS-streamed kernel: 8 (one workgroup per CU) or 4 (two)
 };
 
 struct DecodePlan {

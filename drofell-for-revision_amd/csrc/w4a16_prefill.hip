@@ -46,10 +46,9 @@ namespace dw4 {
 
 namespace {
 
-constexpr int kWaves = 8;
 constexpr int kPairs = 2;                     // strip pairs of one column group
 constexpr int kGroupStrips = 2 * kPairs;      // 16-column strips of one column group
-constexpr int kLdsMax = 160 * 1024;
+constexpr int kLdsMax = 160 * 1024;  // per CU: one 8-wave workgroup, or two 4-wave ones
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -84,8 +83,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // activation tile (BM rows of 256 bytes, 16-byte units of row r stored at
 // position u ^ (r & 15)), the tile's packed weight strips (1 KiB each,
 // lane-linear), then the scale and zero words of each column group.
-template <int MTW, int CG, int GPC>
+template <int MTW, int CG, int GPC, int W>
 struct Tile {
+  static constexpr int kWaves = W;                          // waves per workgroup
+  static constexpr int kLds = W == 8 ? kLdsMax : kLdsMax / 2;  // this workgroup's share
   static constexpr int kBM = 32 * MTW;
   static constexpr int kBN = 64 * CG;
   static constexpr int kAccSlots = MTW * kPairs * 16;       // accumulator floats per lane
@@ -103,7 +104,7 @@ struct Tile {
   static constexpr int kAInstr = kA / (kWaves * 1024);      // 16-byte copies per wave
   static constexpr int kBInstr = kStrips / kWaves;          // strips copied per wave
   static constexpr int kPerChunk = kAInstr + kBInstr + kMetaInstr;  // copies per wave per chunk
-  static constexpr int kDepth = kLdsMax / kBytes < 4 ? kLdsMax / kBytes : 4;
+  static constexpr int kDepth = kLds / kBytes < 4 ? kLds / kBytes : 4;
   // groups of one chunk a wave's k-slice spans
   static constexpr int kGroups = kSteps * GPC / 8 > 0 ? kSteps * GPC / 8 : 1;
   static_assert(kStrips % kWaves == 0 && kKS * CG == kWaves, "wave roles cover the tile");
@@ -111,15 +112,16 @@ struct Tile {
 
 }  // namespace
 
-template <int MTW, int CG, int GPC>
-__global__ void __launch_bounds__(512)
+template <int MTW, int CG, int GPC, int W>
+__global__ void __launch_bounds__(W * 64)
 prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                 const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
                 const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
                 uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ res,
                 int64_t ldres, float* __restrict__ part, int K, int N, int gs, int G,
                 int chunks_per_split, int mtiles, int ntiles) {
-  using T = Tile<MTW, CG, GPC>;
+  using T = Tile<MTW, CG, GPC, W>;
+  constexpr int kWaves = W;
   constexpr int kBM = T::kBM;
   constexpr int kMT = MTW;
   constexpr int kAccSlots = T::kAccSlots;
@@ -127,7 +129,7 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   constexpr int NT = T::kSteps;
   constexpr int KS = T::kKS;
   constexpr int BN = T::kBN;
-  static_assert(S >= 2 && S * T::kBytes <= kLdsMax, "LDS ring fits the CU");
+  static_assert(S >= 2 && S * T::kBytes <= T::kLds, "LDS ring fits the workgroup's share");
   __shared__ __attribute__((aligned(256))) unsigned char ring[S * T::kBytes];
 
   // XCD-aware tile order: the row tiles of one column tile (and all their
@@ -443,9 +445,9 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   }
 }
 
-template <int MTW, int CG, int GPC>
+template <int MTW, int CG, int GPC, int W>
 static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
-  using T = Tile<MTW, CG, GPC>;
+  using T = Tile<MTW, CG, GPC, W>;
   const int mtiles = (a.M + T::kBM - 1) / T::kBM;
   const int ntiles = (a.N + T::kBN - 1) / T::kBN;
   const int KC = a.K / kChunkK;
@@ -455,7 +457,7 @@ static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, h
                     ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
                     : nullptr;
   const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
-  prefill2_kernel<MTW, CG, GPC><<<grid, kWaves * 64, 0, stream>>>(
+  prefill2_kernel<MTW, CG, GPC, W><<<grid, W * 64, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps, a.bias,
       a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
   const hipError_t e = hipGetLastError();
@@ -464,21 +466,25 @@ static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, h
                               stream);
 }
 
-template <int MTW, int CG>
+template <int MTW, int CG, int W>
 static hipError_t launch_prefill2_tile(const GemmArgs& a, int splits, void* ws,
                                        hipStream_t stream) {
   const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
-  if (gpc == 1) return launch_prefill2_cfg<MTW, CG, 1>(a, splits, ws, stream);
-  if (gpc == 2) return launch_prefill2_cfg<MTW, CG, 2>(a, splits, ws, stream);
-  return launch_prefill2_cfg<MTW, CG, 4>(a, splits, ws, stream);
+  if (gpc == 1) return launch_prefill2_cfg<MTW, CG, 1, W>(a, splits, ws, stream);
+  if (gpc == 2) return launch_prefill2_cfg<MTW, CG, 2, W>(a, splits, ws, stream);
+  return launch_prefill2_cfg<MTW, CG, 4, W>(a, splits, ws, stream);
 }
 
 hipError_t launch_prefill2(const GemmArgs& a, const PrefillPlan& plan, void* ws,
                            hipStream_t stream) {
   if (a.perm != nullptr) return hipErrorInvalidValue;  // x must already be in packed row order
-  if (plan.bm == 64 && plan.bn == 256) return launch_prefill2_tile<2, 4>(a, plan.splits, ws, stream);
-  if (plan.bm == 128 && plan.bn == 256) return launch_prefill2_tile<4, 4>(a, plan.splits, ws, stream);
-  if (plan.bm == 128 && plan.bn == 128) return launch_prefill2_tile<4, 2>(a, plan.splits, ws, stream);
+  if (plan.waves == 4) {  // two workgroups per CU
+    if (plan.bm == 64 && plan.bn == 128) return launch_prefill2_tile<2, 2, 4>(a, plan.splits, ws, stream);
+    return hipErrorInvalidValue;
+  }
+  if (plan.bm == 64 && plan.bn == 256) return launch_prefill2_tile<2, 4, 8>(a, plan.splits, ws, stream);
+  if (plan.bm == 128 && plan.bn == 256) return launch_prefill2_tile<4, 4, 8>(a, plan.splits, ws, stream);
+  if (plan.bm == 128 && plan.bn == 128) return launch_prefill2_tile<4, 2, 8>(a, plan.splits, ws, stream);
   return hipErrorInvalidValue;
 }
 

@@ -338,17 +338,20 @@ def test_prefill_7b_large_m(hip_device, kn):
 @pytest.mark.parametrize("k,n,m,g,act", [(1024, 400, 600, 128, False), (2048, 4112, 1000, 128, False),
                                          (1024, 400, 700, 64, True), (1024, 272, 520, 32, True),
                                          (1024, 400, 300, 64, True), (1024, 272, 200, 32, False),
-                                         (1024, 4112, 2000, 32, True), (2048, 4112, 2000, 64, False)],
+                                         (1024, 4112, 2000, 32, True), (2048, 4112, 2000, 64, False),
+                                         (4096, 4112, 200, 128, False), (4096, 2064, 300, 32, True)],
                          ids=["1024x400_M600", "2048x4112_M1000", "1024x400_M700_g64_act",
                               "1024x272_M520_g32_act", "1024x400_M300_g64_act",
                               "1024x272_M200_g32", "1024x4112_M2000_g32_act",
-                              "2048x4112_M2000_g64"])
+                              "2048x4112_M2000_g64", "4096x4112_M200_4wave",
+                              "4096x2064_M300_g32_act_4wave"])
 def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
-    """The LDS-streamed kernel's three tile shapes -- 64 x 256 (M = 200,
-    300), 128 x 128 (M = 520 .. 1000), 128 x 256 (M = 2000, where it needs
-    fewer rounds of workgroups) -- with a partial last row tile, a partial
-    last column tile (N not a multiple of the tile width) and group sizes
-    32 / 64 / 128, unsplit and split along K."""
+    """The LDS-streamed kernel's tile shapes -- 64 x 256 (M = 200, 300),
+    128 x 128 (M = 520 .. 1000), 128 x 256 (M = 2000, where it needs fewer
+    rounds of workgroups) and the 4-wave 64 x 128 workgroups that K = 4096
+    takes where they need fewer K splits -- with a partial last row tile, a
+    partial last column tile (N not a multiple of the tile width) and group
+    sizes 32 / 64 / 128, unsplit and split along K."""
     lay, w = oracle_w(k, n, g, 5000 + m, False, act)
     q4 = build(lay, hip_device)
     for split in (0, 1, 2):
