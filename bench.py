@@ -214,6 +214,51 @@ def stream_ceiling(dev, steps: int) -> list:
     return out
 
 
+def device_peaks(dev, steps: int) -> dict:
+    """What this box reaches outside the W4A16 kernels, as context for the
+    roofline fractions (which stay against the spec peaks): a large fp16
+    library GEMM (torch.matmul, hipBLASLt), a 1 GiB device copy and the
+    library's streaming read over 1 GiB, each captured in a HIP graph."""
+    import subprocess
+
+    import torch
+    from hip_extends import _lib
+
+    props = torch.cuda.get_device_properties(dev)
+    rec = {"device": props.name, "arch": getattr(props, "gcnArchName", ""),
+           "cus": props.multi_processor_count, "hip": torch.version.hip, "torch": torch.__version__}
+    gemm = {}
+    for n in (4096, 8192, 16384):
+        a = torch.randn(n, n, device=dev).to(torch.float16)
+        b = torch.randn(n, n, device=dev).to(torch.float16)
+        c = torch.empty(n, n, device=dev, dtype=torch.float16)
+        ms = time_callable(lambda: torch.matmul(a, b, out=c), max(5, steps // 5), 3, dev)
+        gemm[str(n)] = {"ms": round(ms, 4), "TFLOP/s": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)}
+        del a, b, c
+    rec["fp16_gemm_square"] = gemm
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    ms = time_callable(lambda: dst.copy_(src), max(5, steps // 5), 3, dev)
+    rec["copy_1GiB"] = {"ms": round(ms, 4), "GB/s (read + write)": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+    del dst
+    lib = _lib.load()
+    sink = torch.zeros(2048 * 256, dtype=torch.int32, device=dev)
+    ms = time_callable(lambda: _lib.check("dw4_stream_read", lib.dw4_stream_read(
+        src.data_ptr(), nbytes, 2048, 256, 0x9E3779B9, sink.data_ptr(),
+        torch.cuda.current_stream(dev).cuda_stream)), max(5, steps // 5), 3, dev)
+    rec["stream_read_1GiB"] = {"ms": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    del src, sink
+    torch.cuda.empty_cache()
+    try:  # current clocks, as the SMI reports them (informational)
+        smi = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20)
+        rec["clocks"] = [ln.strip() for ln in smi.stdout.splitlines() if "Mhz" in ln or "MHz" in ln][:8]
+    except (OSError, subprocess.SubprocessError):
+        rec["clocks"] = None
+    log(json.dumps({"device_peaks": rec}))
+    return rec
+
+
 def crossover(mats, dev, steps: int, ms_list=(64, 128, 256, 512, 768, 1024, 2048, 4096, 8192)):
     """Per M: the 56-matrix pass through the native W4A16 kernel, through the
     reference's dense route (bit-exact dequantisation into one shared fp16
@@ -620,6 +665,9 @@ def main() -> int:
                          "shapes and exit")
     ap.add_argument("--crossover", action="store_true",
                     help="only time the 56-matrix pass native vs dense routes over M and exit")
+    ap.add_argument("--peaks", action="store_true",
+                    help="only time a large fp16 library GEMM, a 1 GiB copy and a 1 GiB "
+                         "streaming read on this box, print them and exit")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run 5 plain device copies of this many bytes (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
@@ -645,6 +693,9 @@ def main() -> int:
         return 0
     if args.stream_ceiling:
         stream_ceiling(dev, args.steps)
+        return 0
+    if args.peaks:
+        device_peaks(dev, args.steps)
         return 0
     log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
     mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1))
