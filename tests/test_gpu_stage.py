@@ -200,30 +200,31 @@ def test_fused_stage_calls(hip_device):
         check(out, out_ref, f"mlp out bsz={bsz}")
 
 
-def test_fused_stage_graph_replay(hip_device):
+@pytest.mark.parametrize("rows", [4, 8])
+def test_fused_stage_graph_replay(hip_device, rows):
     """The stage calls captured into a HIP graph: every replay matches eager."""
     qkv, gate, up, down = _stage_layers()
     q4s = build([lw[0] for lw in qkv] + [gate[0], up[0], down[0]], hip_device)
     qq, kq, vq, gq, uq, dq = q4s
     dev = hip_device
     wn = norm_weight(4096, 3).to(dev)
-    x = (make_x(4, 4096, seed=800) * 2).to(torch.float16).to(dev)
-    t_rms = torch.empty(4, 4096, dtype=torch.float16, device=dev)
-    t_q, t_k, t_v = (torch.empty(4, 4096, dtype=torch.float16, device=dev) for _ in range(3))
-    t_g = torch.empty(4, 11008, dtype=torch.float16, device=dev)
-    t_u = torch.empty(4, 11008, dtype=torch.float16, device=dev)
-    out = torch.empty(4, 4096, dtype=torch.float16, device=dev)
+    x = (make_x(rows, 4096, seed=800) * 2).to(torch.float16).to(dev)
+    t_rms = torch.empty(rows, 4096, dtype=torch.float16, device=dev)
+    t_q, t_k, t_v = (torch.empty(rows, 4096, dtype=torch.float16, device=dev) for _ in range(3))
+    t_g = torch.empty(rows, 11008, dtype=torch.float16, device=dev)
+    t_u = torch.empty(rows, 11008, dtype=torch.float16, device=dev)
+    out = torch.empty(rows, 4096, dtype=torch.float16, device=dev)
 
     def step():
         attention_forward_qkv_stage_v2_py(wn, EPS, qq, kq, vq, t_rms, t_q, t_k, t_v, None, x,
-                                          128, 8, 50, 1, 4)
+                                          128, 8, 50, 1, rows)
         mlp_forward_v2_py(wn, EPS, gq, uq, dq, t_rms, t_g, t_u, None, t_q, out, 128, 8, 50)
 
-    say("stage eager")
+    say(f"stage eager rows={rows}")
     step()
     torch.cuda.synchronize()
     eager = [t.clone() for t in (t_q, t_k, t_v, t_g, out)]
-    say("stage graph capture")
+    say(f"stage graph capture rows={rows}")
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
@@ -234,7 +235,7 @@ def test_fused_stage_graph_replay(hip_device):
     with torch.cuda.graph(g):
         step()
     for r in range(4):
-        say(f"stage graph replay {r}")
+        say(f"stage graph replay {r} rows={rows}")
         for t in (t_q, t_k, t_v, t_g, out):
             t.zero_()
         torch.cuda.synchronize()
