@@ -1,5 +1,6 @@
 // gfx950 W4A16 prefill kernel: 64 x 256, 128 x 128 or 128 x 256 output
-// tiles on v_mfma_f32_32x32x16_f16, activations streamed straight into LDS.
+// tiles (8 waves), or 32 x 128 and 64 x 128 tiles (4 waves, two workgroups
+// per CU) on v_mfma_f32_32x32x16_f16, activations streamed straight into LDS.
 //
 // Replaces, in function, the reference's large-M routes (paths relative to
 // /root/reference/After-Revision-DROFELL): q4_matmul_cudablas_v2
@@ -8,7 +9,8 @@
 // (cuda_extends/vllm/csrc/libtorch_stable/quantization/marlin/marlin.cu).
 //
 // Structure of one workgroup (512 threads, 8 waves, two waves per SIMD so
-// that one wave's MFMAs run while the other waits on LDS or the barrier):
+// that one wave's MFMAs run while the other waits on LDS or the barrier; the
+// 4-wave tiles get the same from two workgroups per CU):
 //   * every wave computes all BM tile rows (MTW = BM / 32 A fragments) for
 //     one 64-column group (two 32-column strip pairs) over a slice of each
 //     chunk's k-steps; the tile has CG column groups and 8 / CG k-slices, and
@@ -119,7 +121,7 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                 const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
                 uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ res,
                 int64_t ldres, float* __restrict__ part, int K, int N, int gs, int G,
-                int chunks_per_split, int mtiles, int ntiles) {
+                int chunks_per_split, int mtiles, int ntiles, int splits) {
   using T = Tile<MTW, CG, GPC, W>;
   constexpr int kWaves = W;
   constexpr int kBM = T::kBM;
@@ -132,14 +134,18 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   static_assert(S >= 2 && S * T::kBytes <= T::kLds, "LDS ring fits the workgroup's share");
   __shared__ __attribute__((aligned(256))) unsigned char ring[S * T::kBytes];
 
-  // XCD-aware tile order: the row tiles of one column tile (and all their
-  // K splits) land on one XCD, which then reads those weights once into its L2
+  // XCD-aware order over units (column tile, K split), u = split * ntiles +
+  // ntile: workgroup b runs on XCD b % 8, and the row tiles of unit u are
+  // the workgroups congruent to u mod 8, so they share that XCD's L2 for the
+  // unit's weights, and every XCD gets ceil(units / 8) units
   const int b = blockIdx.x;
   const int q8 = b / (8 * mtiles);
   const int r8 = b % (8 * mtiles);
   const int mtile = r8 / 8;
-  const int ntile = q8 * 8 + (r8 % 8);
-  if (ntile >= ntiles) return;
+  const int unit = q8 * 8 + (r8 % 8);
+  if (unit >= ntiles * splits) return;
+  const int ntile = unit % ntiles;
+  const int split = unit / ntiles;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -151,7 +157,6 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const int hi = (lane >> 4) & 1;    // which strip of a pair holds this lane's B column
   const int j = lane & 15;
   const int KC = K / kChunkK;
-  const int split = blockIdx.y;
   const int c_begin = split * chunks_per_split;
   const int nchunks = min(KC, c_begin + chunks_per_split) - c_begin;
   const int m0 = mtile * kBM;
@@ -325,11 +330,13 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   __builtin_amdgcn_s_barrier();
 
   // ---- k-slice sums through LDS, in two halves of the accumulators (the
-  // first and the last MTW / 2 A fragments) and rounds that halve the
-  // slices: slices [r, 2r) store, slices [0, r) add.  A wave's half is one
-  // slot of MTW * 2 KiB, [accumulator slot][lane] fp32 (conflict-free).
+  // first and the last MTW * kPairs / 2 of the MTW x kPairs fragments, in
+  // row-tile-major order) and rounds that halve the slices: slices [r, 2r)
+  // store, slices [0, r) add.  A wave's half is one slot of MTW * 2 KiB,
+  // [accumulator slot][lane] fp32 (conflict-free).
   constexpr int kHalfSlots = kAccSlots / 2;
   static_assert(KS / 2 * CG * kHalfSlots * 64 * 4 <= S * T::kBytes, "sum slots fit the ring");
+  constexpr int F = kMT * kPairs;  // accumulators per lane, 16 floats each
 #pragma unroll
   for (int part = 0; part < 2; ++part) {
 #pragma unroll
@@ -338,29 +345,24 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
       float* R = reinterpret_cast<float*>(ring) + pos * (kHalfSlots * 64);
       if (ks >= r && ks < 2 * r) {
 #pragma unroll
-        for (int mh = 0; mh < kMT / 2; ++mh)
+        for (int fh = 0; fh < F / 2; ++fh)
 #pragma unroll
-          for (int p = 0; p < kPairs; ++p)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              R[((mh * kPairs + p) * 16 + i) * 64 + lane] = acc[part * kMT / 2 + mh][p][i];
+          for (int i = 0; i < 16; ++i)
+            R[(fh * 16 + i) * 64 + lane] = acc[(part * F / 2 + fh) / kPairs][(part * F / 2 + fh) % kPairs][i];
       }
       __syncthreads();
       if (ks < r) {
 #pragma unroll
-        for (int mh = 0; mh < kMT / 2; ++mh)
+        for (int fh = 0; fh < F / 2; ++fh)
 #pragma unroll
-          for (int p = 0; p < kPairs; ++p)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              acc[part * kMT / 2 + mh][p][i] += R[((mh * kPairs + p) * 16 + i) * 64 + lane];
+          for (int i = 0; i < 16; ++i)
+            acc[(part * F / 2 + fh) / kPairs][(part * F / 2 + fh) % kPairs][i] += R[(fh * 16 + i) * 64 + lane];
       }
       __syncthreads();
     }
   }
   const bool owner = ks == 0;  // waves holding the final sums
 
-  const int splits = gridDim.y;
   if (splits > 1) {
     // ---- split-K: this split's fp32 partial product into plane `split` of
     // [splits][M][N] (a store instruction covers 32 consecutive columns of
@@ -456,10 +458,11 @@ static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, h
   float* part = real_splits > 1
                     ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
                     : nullptr;
-  const dim3 grid((unsigned)(((ntiles + 7) / 8) * 8 * mtiles), (unsigned)real_splits);
+  const int units = ntiles * real_splits;
+  const dim3 grid((unsigned)(((units + 7) / 8) * 8 * mtiles));
   prefill2_kernel<MTW, CG, GPC, W><<<grid, W * 64, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps, a.bias,
-      a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles);
+      a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles, real_splits);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || real_splits == 1) return e;
   return launch_reduce_planes(part, real_splits, a.M, a.N, a.bias, a.y, a.ldy, a.res, a.ldres,
@@ -480,6 +483,7 @@ hipError_t launch_prefill2(const GemmArgs& a, const PrefillPlan& plan, void* ws,
   if (a.perm != nullptr) return hipErrorInvalidValue;  // x must already be in packed row order
   if (plan.waves == 4) {  // two workgroups per CU
     if (plan.bm == 64 && plan.bn == 128) return launch_prefill2_tile<2, 2, 4>(a, plan.splits, ws, stream);
+    if (plan.bm == 32 && plan.bn == 128) return launch_prefill2_tile<1, 2, 4>(a, plan.splits, ws, stream);
     return hipErrorInvalidValue;
   }
   if (plan.bm == 64 && plan.bn == 256) return launch_prefill2_tile<2, 4, 8>(a, plan.splits, ws, stream);

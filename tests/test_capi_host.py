@@ -174,10 +174,15 @@ def test_workspace_size_rules():
     assert _lib.workspace_size(1, 13824, 5120, 128, True) == head + 13824 * 2
     assert _lib.workspace_size(8, 13824, 5120, 128, True) == head + 8 * 13824 * 2
     assert _lib.workspace_size(5, 4096, 4096, 128, True) == head + 5 * 4096 * 2
-    # prefill: the gathered activations follow the split-K area (256-aligned)
-    split = _lib.workspace_size(256, 4096, 4096, 128, False)
-    assert _lib.workspace_size(256, 4096, 4096, 128, True) == \
-        (split + 255) // 256 * 256 + 256 * 4096 * 2
+    # prefill: the gathered activations follow the split-K area, or the
+    # counter head where the call is unsplit (256-aligned).  M=256 at K=4096
+    # runs unsplit 32 x 128 tiles; 11008x4096 at M=256 splits K four ways
+    assert _lib.workspace_size(256, 4096, 4096, 128, False) == 0
+    assert _lib.workspace_size(256, 4096, 4096, 128, True) == head + 256 * 4096 * 2
+    split = _lib.workspace_size(256, 11008, 4096, 128, False)
+    assert split == head + 4 * 256 * 4096 * 4
+    assert _lib.workspace_size(256, 11008, 4096, 128, True) == \
+        (split + 255) // 256 * 256 + 256 * 11008 * 2
     # the per-matrix query covers every M up to max_m, gather included
     assert _lib.query_sizes(5120, 13824, 128, True, 64)["workspace"] >= 64 * 5120 * 2
     # the automatic path takes decode up to M = 48, and up to M = 64 when
@@ -192,7 +197,7 @@ def test_workspace_size_rules():
     head = 4096 * 4
     ws = _lib.workspace_size(4, 13824, 5120, 128, False)
     assert ws > head and (ws - head) % (4 * 5120 * 4) == 0
-    ws = _lib.workspace_size(256, 4096, 4096, 128, False)
+    ws = _lib.workspace_size(256, 11008, 4096, 128, False)
     plane = 256 * 4096 * 4
     assert ws > head + plane and (ws - head) % plane == 0
 

@@ -339,19 +339,24 @@ def test_prefill_7b_large_m(hip_device, kn):
                                          (1024, 400, 700, 64, True), (1024, 272, 520, 32, True),
                                          (1024, 400, 300, 64, True), (1024, 272, 200, 32, False),
                                          (1024, 4112, 2000, 32, True), (2048, 4112, 2000, 64, False),
-                                         (4096, 4112, 200, 128, False), (4096, 2064, 300, 32, True)],
+                                         (4096, 4112, 200, 128, False), (4096, 2064, 300, 32, True),
+                                         (2048, 4112, 400, 128, False), (4096, 1040, 250, 64, False),
+                                         (4096, 4112, 160, 128, True)],
                          ids=["1024x400_M600", "2048x4112_M1000", "1024x400_M700_g64_act",
                               "1024x272_M520_g32_act", "1024x400_M300_g64_act",
                               "1024x272_M200_g32", "1024x4112_M2000_g32_act",
-                              "2048x4112_M2000_g64", "4096x4112_M200_4wave",
-                              "4096x2064_M300_g32_act_4wave"])
+                              "2048x4112_M2000_g64", "4096x4112_M200_32row",
+                              "4096x2064_M300_g32_act_4wave", "2048x4112_M400_4wave",
+                              "4096x1040_M250_g64_32row", "4096x4112_M160_act_32row"])
 def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
-    """The LDS-streamed kernel's tile shapes -- 64 x 256 (M = 200, 300),
+    """The LDS-streamed kernel's tile shapes -- 64 x 256 (M = 300 at K = 1024),
     128 x 128 (M = 520 .. 1000), 128 x 256 (M = 2000, where it needs fewer
-    rounds of workgroups) and the 4-wave 64 x 128 workgroups that K = 4096
-    takes where they need fewer K splits -- with a partial last row tile, a
-    partial last column tile (N not a multiple of the tile width) and group
-    sizes 32 / 64 / 128, unsplit and split along K."""
+    rounds of workgroups), the 4-wave 64 x 128 workgroups that K <= 4096
+    takes where they need fewer K splits (M = 300, 400) and the 4-wave
+    32 x 128 workgroups of M <= 256 at K <= 4096 -- with a partial last row
+    tile, a partial last column tile (N not a multiple of the tile width) and
+    group sizes 32 / 64 / 128, unsplit and split along K (the splits of a
+    column tile spread over the XCDs as units of their own)."""
     lay, w = oracle_w(k, n, g, 5000 + m, False, act)
     q4 = build(lay, hip_device)
     for split in (0, 1, 2):

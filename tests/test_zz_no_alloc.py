@@ -62,12 +62,12 @@ def _both(q4, m, seed):
 
 @pytest.mark.parametrize("act", [False, True], ids=["plain", "act"])
 def test_noalloc_matches_gemm_two_calls(hip_device, act):
-    """First call: M=256 on 4096x4096 (split-K prefill: partial planes and
+    """First call: M=256 on 8192x4096 (split-K prefill: partial planes and
     arrival counters in the scratch; act-order also gathers x there).  Second
     call, smaller: M=40 on 4096x2048, then M=1 decode."""
-    big = _matrix(hip_device, 4096, 4096, act, 61)
+    big = _matrix(hip_device, 8192, 4096, act, 61)
     small = _matrix(hip_device, 4096, 2048, act, 62)
-    assert _lib.workspace_size(256, 4096, 4096, 128, act) > 0  # the scratch is really used
+    assert _lib.workspace_size(256, 8192, 4096, 128, False) > 0  # the scratch is really used
     for q4, m in ((big, 256), (small, 40), (small, 1), (big, 256)):
         say(f"noalloc vs gemm {q4.height}x{q4.width} M={m} act={act}")
         y_ref, y = _both(q4, m, seed=m + 3 * act)
