@@ -38,7 +38,7 @@ def log(msg: str) -> None:
 
 
 def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None,
-                   scale_mul: float = 0.01, act_order: bool = False):
+                   scale_mul: float = 0.01, act_order: bool = False, symmetric: bool = False):
     import torch
     from gptq_synth import LLAMA2_7B_SHAPES
     from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
@@ -56,6 +56,8 @@ def build_matrices(dev, layers: int, max_m: int, seed0: int = 1234, shapes=None,
                                     device=dev, generator=gen)
             qzeros = torch.randint(-2 ** 31, 2 ** 31, (groups, n // 8), dtype=torch.int32,
                                    device=dev, generator=gen)
+            if symmetric:  # config 1: every stored zero 7 (effective zero 8)
+                qzeros.fill_(0x77777777)
             scales = (torch.randn(groups, n, device=dev, generator=gen).abs() * scale_mul
                       + scale_mul / 10).to(torch.float16)
             g_idx = None
@@ -611,11 +613,13 @@ def time_transpose(mats, m: int, steps: int, warmup: int, dev, dense: bool = Fal
 def sweep(mats, dev, steps: int, warmup: int,
           shapes=((4096, 4096), (4096, 11008), (11008, 4096)),
           ms_list=(1, 2, 4, 8, 16, 64, 256, 1024, 2048), act_order: bool = False,
-          tag: str = "") -> None:
+          tag: str = "") -> list:
     """Per-shape, per-M lines (JSON on stderr): mean per launch over the
     rotated matrices of that shape, and the median / p10 / p90 of single
-    graph replays (each replay = one launch per matrix of the shape)."""
+    graph replays (each replay = one launch per matrix of the shape).
+    Returns the lines as dicts."""
     from gptq_synth import algorithmic_bytes, flops
+    out = []
     for (k, n) in shapes:
         for m in ms_list:
             reps = []
@@ -630,11 +634,58 @@ def sweep(mats, dev, steps: int, warmup: int,
             bound = "hbm" if b / HBM_PEAK_GBS * 1e-3 >= f / MFMA_FP16_PEAK_TFLOPS * 1e-6 else "mfma"
             frac = (b / per / 1e3 / HBM_PEAK_GBS) if bound == "hbm" else \
                 (f / per / 1e6 / MFMA_FP16_PEAK_TFLOPS)
-            log(json.dumps({"config": tag, "shape": f"{k}x{n}", "m": m, "act_order": act_order,
-                            "matrices": len(sel), "us": round(per, 3), "median_us": pct(0.5),
-                            "p10_us": pct(0.1), "p90_us": pct(0.9),
-                            "GB/s": round(b / per / 1e3, 1), "TFLOP/s": round(f / per / 1e6, 2),
-                            "bound": bound, "frac": round(frac, 4)}))
+            rec = {"config": tag, "shape": f"{k}x{n}", "m": m, "act_order": act_order,
+                   "matrices": len(sel), "us": round(per, 3), "median_us": pct(0.5),
+                   "p10_us": pct(0.1), "p90_us": pct(0.9),
+                   "GB/s": round(b / per / 1e3, 1), "TFLOP/s": round(f / per / 1e6, 2),
+                   "bound": bound, "frac": round(frac, 4)}
+            log(json.dumps(rec))
+            out.append(rec)
+    return out
+
+
+# BASELINE.json configs 1-4 as the default run measures them: (tag, shape,
+# act-order, symmetric zeros, M values).  Config 5 is the stage leg.
+CONFIG_PLAN = (
+    ("C1", (4096, 4096), False, True, (1,)),
+    ("C2", (4096, 4096), False, False, (1, 2, 4, 8, 16)),
+    ("C3", (4096, 4096), False, False, (16, 64, 256, 1024, 2048)),
+    ("C2", (4096, 11008), False, False, (1, 2, 4, 8, 16)),
+    ("C3", (4096, 11008), False, False, (16, 64, 256, 1024, 2048)),
+    ("C2", (11008, 4096), False, False, (1, 2, 4, 8, 16)),
+    ("C3", (11008, 4096), False, False, (16, 64, 256, 1024, 2048)),
+    ("C4", (5120, 5120), True, False, (1, 8, 64)),
+    ("C4", (5120, 13824), True, False, (1, 8, 64)),
+    ("C4", (13824, 5120), True, False, (1, 8, 64)),
+)
+
+
+def config_points(dev, steps: int) -> dict:
+    """Configs 1-4, one entry per (shape, M): [shape, M, us per launch, GB/s,
+    TFLOP/s, bound, fraction of that bound's peak].  Each shape rotates over
+    distinct matrices totalling >= 512 MB, so the 256 MB Infinity Cache
+    cannot serve the weights between launches."""
+    import torch
+    from gptq_synth import algorithmic_bytes
+    res: dict = {}
+    built = {}
+    for tag, (k, n), act, sym, ms_list in CONFIG_PLAN:
+        key = (k, n, act, sym)
+        if key not in built:
+            built.clear()
+            torch.cuda.empty_cache()
+            count = -(-(512 << 20) // algorithmic_bytes(1, k, n, GROUP, act))
+            built[key] = build_matrices(dev, count, 2048, seed0=7000 + k + n + 17 * sym,
+                                        shapes={f"{k}x{n}": (k, n)}, act_order=act,
+                                        symmetric=sym)
+        sm, _ = built[key]
+        for r in sweep(sm, dev, steps, 3, shapes=((k, n),), ms_list=ms_list, act_order=act,
+                       tag=tag):
+            res.setdefault(tag, []).append([r["shape"], r["m"], r["us"], r["GB/s"],
+                                            r["TFLOP/s"], r["bound"], r["frac"]])
+    built.clear()
+    torch.cuda.empty_cache()
+    return res
 
 
 def main() -> int:
@@ -652,6 +703,8 @@ def main() -> int:
     ap.add_argument("--only-prefill", action="store_true",
                     help="run only the M=--prefill-m leg (for hardware-counter passes)")
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config points (configs 1-4) of the JSON line")
     ap.add_argument("--no-transpose", action="store_true",
                     help="skip the transposed (PEFT backward) leg")
     ap.add_argument("--no-stage", action="store_true",
@@ -796,6 +849,11 @@ def main() -> int:
                   act_order=act, tag=tag)
             del sm, sc
             torch.cuda.empty_cache()
+
+    if not args.no_configs and not args.sweep:
+        result["configs"] = config_points(dev, max(5, args.steps // 5))
+        result["configs_columns"] = ["shape", "m", "us_per_launch", "GB/s", "TFLOP/s", "bound",
+                                     "frac_of_bound_peak"]
 
     if not args.no_transpose:
         # PEFT backward through the same 56 frozen matrices at M=16
