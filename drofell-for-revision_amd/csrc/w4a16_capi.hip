@@ -354,8 +354,13 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
       if (!aligned16(workspace)) return DW4_ERR_MISALIGNED;
       part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + dw4::kWsHeadBytes);
     }
-    const int e = gather_after(need);
-    if (e != DW4_OK) return e;
+    // act-order M = 1: the staged kernel gathers from an LDS copy of x where
+    // it fits (no gather launch); otherwise x is gathered into the workspace
+    if (perm != nullptr) dw4::plan_decode_xg(plan, m, k, n, group_size, cu_count());
+    if (!plan.xg) {
+      const int e = gather_after(need);
+      if (e != DW4_OK) return e;
+    }
     return status_of(dw4::launch_decode(a, plan, part, s));
   }
 

@@ -31,6 +31,11 @@ constexpr int kMetaWords = kMetaBytes / 4;
 constexpr int kDecodeUMax = DW4_DECODE_UMAX;
 constexpr int kDecodeNarrowWaves = DW4_DECODE_NARROW_WAVES;
 constexpr size_t kLdsPerCu = 160 * 1024;
+// Act-order decode at M = 1 (XG): the staged kernel copies the activation
+// row (K <= kXgMaxK) into LDS and each lane gathers at most kXgUnits 16-byte
+// units from it by perm, so a wave stages at most kXgUnits * 4 chunks.
+constexpr int kXgMaxK = 16384;
+constexpr int kXgUnits = 4;
 
 struct GemmArgs {
   int M, K, N, gs, G;
@@ -89,6 +94,7 @@ struct DecodePlan {
   size_t smem;  // dynamic LDS bytes per workgroup
   bool reg = false;  // register-fed kernel (activations not staged in LDS)
   int ss = 1;        // strips per workgroup of the register-fed kernel
+  bool xg = false;   // act-order M = 1: gather from an LDS copy of x (+ K * 2 bytes of LDS)
 };
 constexpr int kDecodeRegMinM = DW4_DECODE_REG_MIN_M;
 
@@ -194,6 +200,22 @@ inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus, bool single 
     }
   }
   return p;
+}
+
+// Act-order M = 1 on the staged kernel: gather from an LDS copy of x (XG)
+// where the copy fits beside the staging regions in the workgroup's LDS share
+// and every wave stages at most kXgUnits * 4 chunks; groups of 128 or more.
+inline void plan_decode_xg(DecodePlan& p, int m, int k, int n, int gs, int cus) {
+  if (p.reg || m != 1 || k > kXgMaxK || gs % kChunkK != 0) return;
+  if ((p.cps + p.waves - 1) / p.waves > kXgUnits * 4) return;
+  const int strips = n / kStripN;
+  const int wgs_per_cu = (strips + cus - 1) / cus;
+  size_t budget = kLdsPerCu / (size_t)(wgs_per_cu > 0 ? wgs_per_cu : 1) - 1024;
+  if (budget > 144 * 1024) budget = 144 * 1024;
+  const size_t smem = p.smem + (size_t)k * 2;
+  if (smem > budget) return;
+  p.xg = true;
+  p.smem = smem;
 }
 
 // DW4_PATH_AUTO's choice.  The decode kernel streams each weight once but

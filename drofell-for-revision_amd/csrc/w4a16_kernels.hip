@@ -126,11 +126,12 @@ constexpr int kLdx = kChunkK + 8;  // halfs per staged activation row (16-byte p
 // GRP: several matrices in one launch (Items table); without it item 0 is
 // read directly, which keeps the item lookup out of a single matrix's
 // prologue (measured ~0.3 us per launch).
-template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP>
+template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP, bool XG>
 __global__ void __launch_bounds__(WAVES * 64)
 decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
               float* __restrict__ part, int K, int gs, int G, int cps, uint32_t mmag,
               uint32_t gmag) {
+  static_assert(!XG || (ACT && MT == 1 && G128 && !GRP), "XG: single-matrix act-order M = 1");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
   const int item = GRP ? item_of(d, blockIdx.x) : 0;
@@ -196,9 +197,34 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   // does not wait for the ring
   h8 xv[kXBatch];
   uint32_t mv[kMBatch];
+  // XG (act-order, M = 1): the activation row is copied whole into LDS after
+  // the reduction region and each wave gathers its units from there by perm,
+  // instead of 8 scattered 2-byte global loads per 16-byte unit.  The copy's
+  // loads and the perm words of this lane's (at most kXgUnits) units are
+  // issued ahead of the weight ring.
+  _Float16* xg = reinterpret_cast<_Float16*>(
+      smem + decode_staged_bytes(M, nch_max, rec, WAVES) + (size_t)WAVES * MT * 1024);
+  constexpr int kXgCopy = (kXgMaxK / 8 + T - 1) / T;
+  h8 xc[XG ? kXgCopy : 1];
+  i4 pw[XG ? kXgUnits : 1][2];
+  if constexpr (XG) {
 #pragma unroll
-  for (int b = 0; b < kXBatch; ++b)
-    if (lane + 64 * b < xunits) xv[b] = x_unit(lane + 64 * b);
+    for (int b = 0; b < kXgCopy; ++b)
+      if (tid + T * b < K / 8) xc[b] = *(const h8*)(x + 8 * (tid + T * b));
+#pragma unroll
+    for (int b = 0; b < kXgUnits; ++b) {
+      const int u = lane + 64 * b;
+      if (u < xunits) {
+        const int k = (c0 + wave + (u >> 4) * WAVES) * kChunkK + (u & 15) * 8;
+        pw[b][0] = *(const i4*)(perm + k);
+        pw[b][1] = *(const i4*)(perm + k + 4);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < kXBatch; ++b)
+      if (lane + 64 * b < xunits) xv[b] = x_unit(lane + 64 * b);
+  }
 #pragma unroll
   for (int b = 0; b < kMBatch; ++b)
     if (lane + 64 * b < munits) mv[b] = m_word(lane + 64 * b);
@@ -227,16 +253,34 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   for (int u = 0; u < U; ++u)
     if (U >= 2 || u < nch) ring_load(qb[u], sb[u], zb[u], u);
 
+  if constexpr (XG) {
 #pragma unroll
-  for (int b = 0; b < kXBatch; ++b)
-    if (lane + 64 * b < xunits) *(h8*)x_dst(lane + 64 * b) = xv[b];
+    for (int b = 0; b < kXgCopy; ++b)
+      if (tid + T * b < K / 8) *(h8*)(xg + 8 * (tid + T * b)) = xc[b];
+    // every wave's copy in LDS before any wave gathers; the weight ring's
+    // loads stay in flight (a __syncthreads would wait for them too)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int b = 0; b < kXgUnits; ++b) {
+      const int u = lane + 64 * b;
+      if (u < xunits) {
+        const i4 p0 = pw[b][0], p1 = pw[b][1];
+        *(h8*)x_dst(u) = h8{xg[p0[0]], xg[p0[1]], xg[p0[2]], xg[p0[3]],
+                            xg[p1[0]], xg[p1[1]], xg[p1[2]], xg[p1[3]]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < kXBatch; ++b)
+      if (lane + 64 * b < xunits) *(h8*)x_dst(lane + 64 * b) = xv[b];
+  }
 #pragma unroll
   for (int b = 0; b < kMBatch; ++b)
     if (lane + 64 * b < munits) mw[lane + 64 * b] = mv[b];
   // The rest (M > 1 or many chunks) in batches: all loads of a batch are in
   // flight before its first store, so the staging costs one L2 round trip
   // per batch rather than one per 16-byte unit.
-  for (int u0 = lane + 64 * kXBatch; u0 < xunits; u0 += 64 * kXBatch) {
+  for (int u0 = lane + 64 * kXBatch; !XG && u0 < xunits; u0 += 64 * kXBatch) {
 #pragma unroll
     for (int b = 0; b < kXBatch; ++b)
       if (u0 + 64 * b < xunits) xv[b] = x_unit(u0 + 64 * b);
@@ -1603,18 +1647,18 @@ hipError_t launch_gather_rows(const uint16_t* x, int64_t ldx, const int32_t* per
   return hipGetLastError();
 }
 
-template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP>
+template <int MT, int WAVES, int U, bool G128, bool ACT, bool GRP, bool XG = false>
 static hipError_t launch_decode_one(const GemmArgs& a, const Items& d, const DecodePlan& p,
                                     float* part, hipStream_t stream) {
   const dim3 grid((unsigned)d.wg0[d.count], p.splits);
   if (p.smem > 64 * 1024) {
     static std::atomic<uint64_t> allowed{0};
     const hipError_t e = allow_lds(
-        reinterpret_cast<const void*>(&decode_kernel<MT, WAVES, U, G128, ACT, GRP>), kLdsPerCu,
-        allowed);
+        reinterpret_cast<const void*>(&decode_kernel<MT, WAVES, U, G128, ACT, GRP, XG>),
+        kLdsPerCu, allowed);
     if (e != hipSuccess) return e;
   }
-  decode_kernel<MT, WAVES, U, G128, ACT, GRP><<<grid, WAVES * 64, p.smem, stream>>>(
+  decode_kernel<MT, WAVES, U, G128, ACT, GRP, XG><<<grid, WAVES * 64, p.smem, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, d, part, a.K, a.gs, a.G, p.cps, div_magic(a.M),
       G128 && a.gs > kChunkK ? div_magic(a.gs / kChunkK) : 0u);
   return hipGetLastError();
@@ -1627,7 +1671,14 @@ static hipError_t launch_decode_cfg(const GroupArgs& g, const DecodePlan& p, flo
   if (p.splits > 1 && g.count != 1) return hipErrorInvalidValue;  // planes of one matrix
   const Items d = make_items(g, 1);
   hipError_t err;
-  if (g.count == 1) {
+  if (p.xg) {  // act-order M = 1 gathering from an LDS copy of x (planner-checked sizes)
+    if constexpr (MT == 1 && ACT && G128) {
+      if (g.count != 1 || a.M != 1 || a.K > kXgMaxK) return hipErrorInvalidValue;
+      err = launch_decode_one<MT, WAVES, U, G128, ACT, false, true>(a, d, p, part, stream);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (g.count == 1) {
     err = launch_decode_one<MT, WAVES, U, G128, ACT, false>(a, d, p, part, stream);
   } else if constexpr (MT == 1) {  // the staged kernel is planned for M <= 4 only
     err = launch_decode_one<MT, WAVES, U, G128, ACT, true>(a, d, p, part, stream);

@@ -16,7 +16,7 @@ import torch
 
 from gptq_synth import make_layer, make_x
 from hip_extends import _lib
-from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams
+from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams, gemm_group
 from oracle import gptq
 
 pytestmark = pytest.mark.gpu
@@ -222,6 +222,41 @@ def test_act_order_13b(hip_device, kn):
             y = q4.matmul(x.to(hip_device), path=path)
             torch.cuda.synchronize()
             check_tol(y, gptq.gemm_ref(x.numpy(), w), f"act {k}x{n} M={m} path {path}")
+
+
+@pytest.mark.parametrize("kn", [(5120, 5120), (13824, 5120), (5120, 13824), (16384, 1024),
+                                (16512, 1024)],
+                         ids=lambda kn: f"{kn[0]}x{kn[1]}")
+def test_act_order_m1_lds_gather(hip_device, kn):
+    """Act-order at M=1: the staged decode kernel copies x into LDS and
+    gathers its units from there by perm (K <= 16384; 16512 takes the gather
+    launch instead).  The same plan through dw4_gemm_group (one item) gathers
+    per workgroup from global memory: the staged values and the sums are the
+    same, so the outputs are bit-identical, and both are within the oracle's
+    tolerance.  No workspace is needed for the LDS gather."""
+    k, n = kn
+    lay, w = oracle_w(k, n, 128, 3100 + k + n, False, True)
+    q4 = build(lay, hip_device)
+    lib = _lib.load()
+    x = make_x(1, k, seed=k + n)
+    xd = x.to(hip_device)
+    ref = gptq.gemm_ref(x.numpy(), w)
+    say(f"act-order M=1 LDS gather {k}x{n}")
+    y = q4.matmul(xd, path=_lib.DW4_PATH_DECODE)
+    torch.cuda.synchronize()
+    check_tol(y, ref, f"act M=1 {k}x{n}")
+    say(f"act-order M=1 {k}x{n}: no workspace")
+    y0 = torch.empty(1, n, dtype=torch.float16, device=hip_device)
+    st = lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 1, k, n, 128, xd.data_ptr(), k,
+                           q4.qweight.data_ptr(), q4.qzeros.data_ptr(), q4.scales.data_ptr(),
+                           q4.perm.data_ptr(), None, y0.data_ptr(), n, None, 0,
+                           torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.DW4_OK, _lib.strerror(st)
+    say(f"act-order M=1 {k}x{n}: grouped launch, per-workgroup gather")
+    (yg,) = gemm_group(xd, [q4])
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), yg.view(torch.int16)), f"{k}x{n}"
+    assert torch.equal(y0.view(torch.int16), yg.view(torch.int16)), f"{k}x{n} no workspace"
 
 
 def test_act_order_gather_first_matches_in_kernel_gather(hip_device):
