@@ -135,7 +135,9 @@ int dw4_query_sizes(int k, int n, int group_size, int act_order, int max_m,
  * it returns 0).  With act_order it includes M*K fp16 for x gathered into
  * the packed row order (placed after the split-K area and the arrival
  * counters); a call whose workspace lacks that room gathers inside every
- * workgroup instead: the same result bit for bit, slower.  For 5 <= M <= 64
+ * workgroup instead: the same result bit for bit, slower.  (At M = 1 with
+ * K <= 16384 the decode kernel gathers from an LDS copy of x and uses none
+ * of the act-order room.)  For 5 <= M <= 64
  * the decode kernel may split K over workgroups (fp32 planes in the
  * workspace); given less than this size it runs unsplit instead (a valid
  * result, summed in another order). */
