@@ -165,10 +165,10 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n) {
   return dw4::split_ws_bytes(p.splits, mt * nt * p.bm * p.bn);
 }
 
-bool use_decode(int path, int m, int n) {
+bool use_decode(int path, int m, int k, int n) {
   if (path == DW4_PATH_DECODE) return true;
   if (path == DW4_PATH_PREFILL) return false;
-  return dw4::auto_decode(m, n, cu_count());
+  return dw4::auto_decode(m, n, cu_count(), k);
 }
 
 // Split-K bytes, then (act-order) the gathered activations: 256-aligned and
@@ -176,7 +176,7 @@ bool use_decode(int path, int m, int n) {
 // next split call on the workspace.
 size_t workspace_for(int path, int m, int k, int n, int group_size, bool act) {
   if (m <= 0) return 0;
-  const bool decode = use_decode(path, m, n);
+  const bool decode = use_decode(path, m, k, n);
   size_t split;
   if (decode) {
     const dw4::DecodePlan p = dw4::plan_decode(m, k, n, group_size, cu_count());
@@ -300,7 +300,7 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
   if (!x || !packed_qweight || !packed_zeros || !packed_scales || !y) return DW4_ERR_INVALID_ARG;
   if (ldx < k || ldy < n) return DW4_ERR_INVALID_ARG;
   if (!aligned16(x) || (ldx % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
-  const bool decode = use_decode(path, m, n);
+  const bool decode = use_decode(path, m, k, n);
   if (decode && m > dw4::kDecodeMaxM) return DW4_ERR_INVALID_ARG;
 
   hipStream_t s = static_cast<hipStream_t>(stream);

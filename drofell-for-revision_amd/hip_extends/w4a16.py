@@ -40,7 +40,8 @@ class TuningParams:
     # Flattened M at or below which the register-dequant decode kernel runs
     # (at most 64: four 16-row MFMA tiles); above it the prefill kernel runs.
     # None leaves the choice to the library: decode up to M = 48, or up to
-    # M = 64 when N / 16 is at most the device's CU count.
+    # M = 64 when N / 16 is at most the device's CU count (or at most 1.25x
+    # it with K <= 8192).
     DECODE_MAX_M: Optional[int] = None
     # Largest flattened M the shared workspace is sized for.  Larger calls
     # still run, with the prefill kernel unsplit along K.

@@ -116,7 +116,8 @@ enum {
 
 /* Path selection for dw4_gemm_path(). */
 enum {
-  DW4_PATH_AUTO = 0,     /* decode for M <= 48, or M <= 64 when N / 16 <= CUs */
+  DW4_PATH_AUTO = 0,     /* decode for M <= 48, or M <= 64 when N / 16 <= CUs (or
+                            <= 1.25 CUs with K <= 8192) */
   DW4_PATH_DECODE = 1,   /* register-dequant MFMA kernel, M <= 64 */
   DW4_PATH_PREFILL = 2   /* LDS-staged MFMA kernel, any M */
 };
