@@ -719,16 +719,19 @@ static hipError_t launch_decode_reg_cfg(const GroupArgs& g, const Items& d, cons
                               stream);
 }
 
-// Deepest ring (chunks in flight per wave) that a variant holds without
-// spilling.  The A fragments of one chunk take 16 * MT registers per lane
-// (their act-order gathers more while in flight) and each strip's weight
-// words 4 more; 16-wave workgroups have 128 registers per lane, 8-wave ones
-// 256.
+// Ring depth (chunks in flight per wave).  Two where the registers hold
+// it: a deeper ring puts more of every wave's A-fragment and weight loads in
+// its first burst, and the waves then wait longer for their first chunk.
+// Measured against four for one row tile (M <= 16): grouped q/k/v M=8 12.3
+// -> 9.8 us, M=16 13.3 -> 10.9; gate/up pair M=16 18.1 -> 16.8;
+// 13824x5120 M=8 17.2 -> 15.3; 4096x11008 M=5 11.3 -> 9.6; no shape slower.
+// The A fragments of one chunk take 16 * MT registers per lane (their
+// act-order gathers more while in flight) and each strip's weight words 4
+// more; 16-wave workgroups have 128 registers per lane, 8-wave ones 256.
 constexpr int decode_reg_umax(int mt, int waves, int ss, int gpc, bool act) {
-  return waves == 16 ? ((act || gpc == 4 || decode_reg_lx(mt, ss, gpc, act)) ? 2 : 4)
-         : ss == 4 && mt == 1 && gpc == 2 ? 2
-         : ss == 4   ? (mt == 1 ? (gpc == 4 ? 2 : 4) : (mt == 2 ? 2 : 1))
-         : mt == 1   ? 4
+  return waves == 16 ? 2
+         : ss == 4   ? (mt <= 2 ? 2 : 1)
+         : mt == 1   ? 2
          : act       ? 1
                      : (mt == 2 ? 2 : 1);
 }
