@@ -115,7 +115,9 @@ def test_after_stage(hip_device, shape, act):
         assert q4s[1].perm.data_ptr() == q4s[2].perm.data_ptr()  # gate/up share: chained
     ws = [lw[1] for lw in lws]
     wn = norm_weight(hidden, 7)
-    ms = (1, 2, 3, 4, 8) if act else (1, 2, 3, 4, 8, 16, 33, 64, 100)
+    # 7B up to M=256: the LDS-streamed prefill tiles' residual epilogues
+    # (32 x 128 for o_proj, 64 x 256 with K splits and the reduce for down)
+    ms = (1, 2, 3, 4, 8) if act else (1, 2, 3, 4, 8, 16, 33, 64, 100, 200, 256)
     b = _Bufs(max(ms), hidden, inter, hip_device)
     for m in ms:
         say(f"after_stage {hidden}x{inter} act={act} M={m}")

@@ -403,6 +403,26 @@ def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
         check_tol(y, gptq.gemm_ref(x.numpy(), w), f"{k}x{n} M={m} split {split}")
 
 
+def test_prefill_bias_lds_streamed_tiles(hip_device):
+    """Bias in the LDS-streamed kernel's epilogues: the 32 x 128 tiles (M=200,
+    256 at K=4096, a partial last column tile), 64 x 256 with K splits (the
+    bias added by the reduce) and unsplit, against the oracle plus bias."""
+    k, n = 4096, 1040
+    lay, w = oracle_w(k, n, 128, 6060, False, False)
+    q4 = build(lay, hip_device)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(6)) * 0.5).half()
+    bd = bias.to(hip_device)
+    for m in (200, 256):
+        for split in (0, 1, 2):
+            say(f"prefill bias {k}x{n} M={m} split={split}")
+            q4.tuning_params = TuningParams(PREFILL_SPLIT_K=split)
+            x = make_x(m, k, seed=m + 606)
+            y = q4.matmul(x.to(hip_device), bias=bd, path=_lib.DW4_PATH_PREFILL)
+            torch.cuda.synchronize()
+            ref = gptq.gemm_ref(x.numpy(), w) + bias.float().numpy()[None, :]
+            check_tol(y, ref, f"bias M={m} split {split}")
+
+
 def test_shared_workspace_across_shapes(hip_device):
     """Two matrices share one workspace; decode split-K partials and prefill
     split-K calls of different tile counts alternate on it.  Each result
