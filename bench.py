@@ -644,8 +644,9 @@ def sweep(mats, dev, steps: int, warmup: int,
     return out
 
 
-# BASELINE.json configs 1-4 as the default run measures them: (tag, shape,
-# act-order, symmetric zeros, M values).  Config 5 is the stage leg.
+# The benchmark's configurations 1-4 as the default run measures them: (tag,
+# shape, act-order, symmetric zeros, M values).  Configuration 5 is the stage
+# leg.
 CONFIG_PLAN = (
     ("C1", (4096, 4096), False, True, (1,)),
     ("C2", (4096, 4096), False, False, (1, 2, 4, 8, 16)),
