@@ -73,11 +73,14 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
                        const int32_t* __restrict__ context_lens,
                        const float* __restrict__ alibi, int part_tokens, int num_parts,
                        float* __restrict__ ws_ml, float* __restrict__ ws_out) {
-  constexpr int SLICES = HS / 8;         // 16-byte slices of a key row
-  constexpr int TPL = 64 / BS;           // slice groups per wave (lanes of one token)
-  constexpr int SPL = SLICES / TPL;      // slices per lane
-  constexpr int DPL = HS / 64;           // value dims per lane
-  static_assert(HS % 64 == 0 && 64 % BS == 0 && SLICES % TPL == 0, "shape");
+  constexpr int SLICES = HS / 8;                 // 16-byte slices of a key row
+  constexpr int TPL = 64 / BS;                   // slice groups per wave (lanes of one token)
+  constexpr int SPL = (SLICES + TPL - 1) / TPL;  // slices per lane (the last may be past HS)
+  constexpr int DPL = (HS + 63) / 64;            // value dims per lane (the last may be past HS)
+  // head sizes that are not multiples of 64 (80, 96, 112) leave some lanes
+  // without a last key slice or value dim: those hold zeros and store nothing
+  constexpr bool KTAIL = SLICES % TPL != 0, VTAIL = HS % 64 != 0;
+  static_assert(HS % 8 == 0 && 64 % BS == 0, "shape");
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int G = num_heads / num_kv_heads;  // query heads per kv head (<= GMAX)
   float* qs = sm;                           // [G][HS] fp32 query (scaled)
@@ -134,7 +137,13 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   auto load_k = [&](int slot, int i) {
     const uint16_t* kb = kbase(i);
 #pragma unroll
-    for (int j = 0; j < SPL; ++j) kreg[slot][j] = *(const h8*)(kb + ((sg + TPL * j) * BS + tt) * 8);
+    for (int j = 0; j < SPL; ++j) {
+      if (KTAIL && sg + TPL * j >= SLICES) {
+        kreg[slot][j] = h8{};
+        continue;
+      }
+      kreg[slot][j] = *(const h8*)(kb + ((sg + TPL * j) * BS + tt) * 8);
+    }
   };
   auto load_v = [&](int slot, int i) {
     const uint16_t* vb = vbase(i);
@@ -142,7 +151,9 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
     for (int j = 0; j < DPL; ++j)
 #pragma unroll
       for (int u = 0; u < BS / 8; ++u)
-        vreg[slot][j][u] = *(const h8*)(vb + (size_t)(lane + 64 * j) * BS + 8 * u);
+        vreg[slot][j][u] = VTAIL && lane + 64 * j >= HS
+                               ? h8{}
+                               : *(const h8*)(vb + (size_t)(lane + 64 * j) * BS + 8 * u);
   };
 #pragma unroll
   for (int u = 0; u < NPF; ++u)
@@ -161,6 +172,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
       if (g < G) {
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
+          if (KTAIL && sg + TPL * j >= SLICES) continue;
           const float* qv = qs + g * HS + (sg + TPL * j) * 8;
 #pragma unroll
           for (int e = 0; e < 8; ++e) dot[g] = fmaf(qv[e], (float)kreg[slot][j][e], dot[g]);
@@ -254,7 +266,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   for (int g = 0; g < GMAX; ++g)
 #pragma unroll
     for (int j = 0; j < DPL; ++j)
-      if (g < G) red[(wave * GMAX + g) * HS + lane + 64 * j] = acc[g][j];
+      if (g < G && (!VTAIL || lane + 64 * j < HS)) red[(wave * GMAX + g) * HS + lane + 64 * j] = acc[g][j];
   __syncthreads();
   for (int i = tid; i < G * HS; i += kAttnThreads) {
     const int g = i / HS, d = i % HS;
@@ -518,6 +530,9 @@ hipError_t launch_paged_attention(const PagedAttnArgs& a, const PagedAttnPlan& p
                                   hipStream_t stream) {
   switch (a.head_size) {
     case 64: return launch_pa_bs<64>(a, p, ws, stream);
+    case 80: return launch_pa_bs<80>(a, p, ws, stream);
+    case 96: return launch_pa_bs<96>(a, p, ws, stream);
+    case 112: return launch_pa_bs<112>(a, p, ws, stream);
     case 128: return launch_pa_bs<128>(a, p, ws, stream);
     case 256: return launch_pa_bs<256>(a, p, ws, stream);
     default: return hipErrorInvalidValue;

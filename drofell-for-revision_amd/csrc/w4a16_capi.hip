@@ -165,6 +165,12 @@ size_t prefill_ws_bytes(const dw4::PrefillPlan& p, int m, int n) {
   return dw4::split_ws_bytes(p.splits, mt * nt * p.bm * p.bn);
 }
 
+// The register-fed decode kernel addresses the rows of x with 32-bit element
+// offsets from x, so its calls need (m - 1) * ldx + k < 2^31.
+bool rows_fit_i32(int m, int64_t ldx, int k) {
+  return (int64_t)(m > 0 ? m - 1 : 0) * ldx + k <= (int64_t)INT32_MAX;
+}
+
 bool use_decode(int path, int m, int k, int n) {
   if (path == DW4_PATH_DECODE) return true;
   if (path == DW4_PATH_PREFILL) return false;
@@ -300,7 +306,11 @@ int gemm_run(int path, int split_k, int m, int k, int n, int group_size, const u
   if (!x || !packed_qweight || !packed_zeros || !packed_scales || !y) return DW4_ERR_INVALID_ARG;
   if (ldx < k || ldy < n) return DW4_ERR_INVALID_ARG;
   if (!aligned16(x) || (ldx % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
-  const bool decode = use_decode(path, m, k, n);
+  // rows of x too far apart for the decode kernel's 32-bit offsets take the
+  // prefill kernel, which addresses rows in 64 bits
+  const bool wide = !rows_fit_i32(m, ldx, k);
+  if (wide && path == DW4_PATH_DECODE) return DW4_ERR_UNSUPPORTED;
+  const bool decode = !wide && use_decode(path, m, k, n);
   if (decode && m > dw4::kDecodeMaxM) return DW4_ERR_INVALID_ARG;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -490,7 +500,8 @@ static int check_attn_shape(int num_seqs, int num_heads, int num_kv_heads, int h
     return DW4_ERR_INVALID_ARG;
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > dw4::kAttnMaxGroup)
     return DW4_ERR_UNSUPPORTED;
-  if ((head_size != 64 && head_size != 128 && head_size != 256) ||
+  if ((head_size != 64 && head_size != 80 && head_size != 96 && head_size != 112 &&
+       head_size != 128 && head_size != 256) ||
       (block_size != 16 && block_size != 32))
     return DW4_ERR_UNSUPPORTED;
   return DW4_OK;
@@ -752,7 +763,8 @@ int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, i
   const int st = check_x(x, ldx, items[0].k);
   if (st != DW4_OK) return st;
   const int cus = cu_count();
-  if (m <= dw4::kGroupDecodeMaxM && dw4::auto_decode(m, n_total, cus)) {
+  if (m <= dw4::kGroupDecodeMaxM && rows_fit_i32(m, ldx, items[0].k) &&
+      dw4::auto_decode(m, n_total, cus)) {
     const dw4::DecodePlan plan =
         dw4::plan_decode(m, items[0].k, n_total, items[0].group_size, cus, false);
     if (plan.splits == 1) {
@@ -783,7 +795,7 @@ int dw4_gemm_silu_mul(int m, const uint16_t* x, int64_t ldx, const dw4_item* gat
   st = check_x(x, ldx, gate->k);
   if (st != DW4_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (m <= dw4::kPairMaxM && gate->perm == up->perm &&
+  if (m <= dw4::kPairMaxM && gate->perm == up->perm && rows_fit_i32(m, ldx, gate->k) &&
       dw4::auto_decode(m, 2 * gate->n, cu_count())) {
     dw4::GroupArgs g{};
     g.count = 2;

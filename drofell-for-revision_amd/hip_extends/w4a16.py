@@ -673,13 +673,16 @@ def attention_forward_rope_stage_v2_py(temp_q_output: torch.Tensor, temp_k_outpu
 def rope_tables(sin: torch.Tensor, cos: torch.Tensor,
                 head_dim: int) -> Tuple[torch.Tensor, torch.Tensor, int]:
     """fp16 sin / cos tables as contiguous [positions, head_dim] and the
-    position count, from tables of any leading shape ending in head_dim
-    ([P, hd] or the rotary modules' [1, 1, P, hd])."""
+    position count, from [P, hd] tables or the rotary modules' [1, 1, P, hd]
+    (every dimension before the last two must be 1: a batched table would
+    otherwise be read as more positions)."""
     if sin.shape != cos.shape:
         raise ValueError(f"sin {tuple(sin.shape)} and cos {tuple(cos.shape)} differ")
-    if sin.dim() < 1 or sin.shape[-1] != head_dim:
-        raise ValueError(f"rope tables end in {sin.shape[-1] if sin.dim() else None}, "
-                         f"head_dim is {head_dim}")
+    if sin.dim() < 2 or sin.shape[-1] != head_dim:
+        raise ValueError(f"rope tables must be [..., positions, {head_dim}], got "
+                         f"{tuple(sin.shape)}")
+    if any(d != 1 for d in sin.shape[:-2]):
+        raise ValueError(f"rope tables {tuple(sin.shape)}: every leading dimension must be 1")
     s16 = sin.to(torch.float16).contiguous().view(-1, head_dim)
     c16 = cos.to(torch.float16).contiguous().view(-1, head_dim)
     return s16, c16, s16.shape[0]

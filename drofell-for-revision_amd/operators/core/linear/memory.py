@@ -25,6 +25,12 @@ constructor arguments and methods.  Each twin holds one
 
 The workspace sizes come from the library's host-only sizing call, so the
 twins need ``libdrofell_w4a16.so`` but no GPU.
+
+One more twin has no module behind it: :class:`W4A16LibraryMemoryModel`,
+the fixed scratch array of ``dw4_gemm_noalloc``, which the library's code
+object carries and which every GPU that runs the library holds once, from
+the library's first use on it until the process ends, whether or not that
+entry point is ever called.  A per-device plan mounts exactly one.
 """
 from __future__ import annotations
 
@@ -53,6 +59,16 @@ class LinearMakerMemoryModel(ABC):
 
 def _workspace_bytes(k: int, n: int, group_size: int, act: bool, max_m: int) -> int:
     return _lib.query_sizes(k, n, group_size, act, max(1, max_m))["workspace"]
+
+
+class W4A16LibraryMemoryModel(MemoryModule):
+    """Twin of the library's per-GPU static device memory: the
+    ``DW4_NOALLOC_SCRATCH_BYTES`` array of ``dw4_gemm_noalloc`` (mount one per
+    device that runs the library, beside the decoder groups' twins)."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        self.noalloc_scratch = MemoryTensor((_lib.NOALLOC_SCRATCH_BYTES,), MemoryUInt8)
 
 
 class CacheV2MemoryModel(MemoryModule):

@@ -187,7 +187,10 @@ int dw4_gemm_path(int path, int split_k, int m, int k, int n, int group_size,
  * that returns DW4_ERR_SCRATCH before launching anything.  Every call on a
  * GPU shares that GPU's array, so calls that overlap in time on one GPU
  * (concurrent streams or threads) race; serialise them.  Calls no hipMalloc,
- * hipFree or allocating library routine. */
+ * hipFree or allocating library routine.  The first call on a GPU sets the
+ * array up (looks up its address and clears its counter head with a kernel
+ * on `stream`): make that call outside HIP graph capture; later calls may
+ * be captured and replayed. */
 #define DW4_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int dw4_gemm_noalloc(int m, int k, int n, int group_size,
                      const uint16_t* x, int64_t ldx,
@@ -357,7 +360,7 @@ int dw4_restore_from_cache(int num_tokens, int num_kv_heads, int head_size, int 
  * [num_seqs][num_heads][head_size] with row strides q_stride, o_stride per
  * sequence; block_tables int32 [num_seqs][max_blocks_per_seq];
  * context_lens int32 [num_seqs], each in 1..max_context_len; alibi_slopes
- * float [num_heads] or NULL.  head_size 64, 128 or 256; num_heads a
+ * float [num_heads] or NULL.  head_size 64, 80, 96, 112, 128 or 256; num_heads a
  * multiple of num_kv_heads with at most 8 query heads per kv head.
  * Softmax and both products in fp32; long contexts are split into
  * partitions combined in a fixed order (deterministic).  workspace: at

@@ -143,6 +143,35 @@ def _fp16_fma(a: np.float16, b: np.float16, c: np.float16) -> np.float16:
     return fp16_round(exact)
 
 
+def fp16_fma(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Elementwise ``a * b + c`` of fp16 arrays with one rounding to fp16
+    (the vector form of :func:`_fp16_fma`, which pins it).
+
+    The product of two fp16 values is exact in float64; Knuth's TwoSum
+    gives ``p + c = s + err`` exactly with ``s`` the float64 sum.  Rounding
+    ``s`` to fp16 (numpy: to nearest, ties to even) is the correct rounding
+    of ``s + err`` except when ``s`` is exactly halfway between two fp16
+    values and ``err`` is not zero: every such midpoint is a float64 value,
+    so ``s + err`` cannot lie beyond one, and then ``err``'s sign picks the
+    neighbour.  Signed zeros follow IEEE addition of the float64 values."""
+    a64 = np.asarray(a, np.float16).astype(np.float64)
+    b64 = np.asarray(b, np.float16).astype(np.float64)
+    c64 = np.asarray(c, np.float16).astype(np.float64)
+    p = a64 * b64
+    s = p + c64
+    bb = s - p
+    err = (p - (s - bb)) + (c64 - bb)
+    with np.errstate(over="ignore"):
+        r = s.astype(np.float16)
+        up = np.nextafter(r, np.float16(np.inf))
+        down = np.nextafter(r, np.float16(-np.inf))
+    other = np.where(s > r.astype(np.float64), up, down)
+    mid = (r.astype(np.float64) + other.astype(np.float64)) / 2
+    tie = (s == mid) & (err != 0) & np.isfinite(r) & np.isfinite(other)
+    toward_other = np.sign(err) == np.sign(other.astype(np.float64) - r.astype(np.float64))
+    return np.where(tie & toward_other, other, r)
+
+
 def rope(x: np.ndarray, sin: np.ndarray, cos: np.ndarray, num_heads: int, past_len: int,
          past_lens: Optional[np.ndarray] = None) -> np.ndarray:
     """``cuda_extends/exllama/fuse_v2/rope.cu:24-91`` on fp16 x
@@ -150,23 +179,26 @@ def rope(x: np.ndarray, sin: np.ndarray, cos: np.ndarray, num_heads: int, past_l
     ``past + row // heads``; pair (l, r) = (x[c], x[c + hd/2]):
     ``l' = fma(l, cos[c], fp16(r * -sin[c]))``,
     ``r' = fma(r, cos[c + hd/2], fp16(l * sin[c + hd/2]))``, every product
-    and fma rounded once to fp16.  Rows whose position falls outside the
-    tables are returned unchanged."""
+    and fma rounded once to fp16 (:func:`fp16_fma`).  Rows whose position
+    falls outside the tables are returned unchanged."""
     out = x.copy()
     batch, rows, hd = x.shape
     half = hd // 2
     for b in range(batch):
         base = past_len if past_len >= 0 else int(past_lens[b])
-        for r in range(rows):
-            pos = base + r // num_heads
-            if pos < 0 or pos >= sin.shape[0]:
-                continue
-            for c in range(half):
-                lv, rv = x[b, r, c], x[b, r, c + half]
-                ls = np.float16(np.float32(rv) * -np.float32(sin[pos, c]))  # exact product, one rounding
-                rs = np.float16(np.float32(lv) * np.float32(sin[pos, c + half]))
-                out[b, r, c] = _fp16_fma(lv, cos[pos, c], ls)
-                out[b, r, c + half] = _fp16_fma(rv, cos[pos, c + half], rs)
+        pos = base + np.arange(rows) // num_heads
+        ok = (pos >= 0) & (pos < sin.shape[0])
+        if not ok.any():
+            continue
+        p = pos[ok]
+        lv, rv = x[b, ok, :half], x[b, ok, half:]
+        s_lo, s_hi = sin[p, :half], sin[p, half:]
+        c_lo, c_hi = cos[p, :half], cos[p, half:]
+        # fp16 operands: each float32 product is exact, then rounded once
+        ls = (rv.astype(np.float32) * -s_lo.astype(np.float32)).astype(np.float16)
+        rs = (lv.astype(np.float32) * s_hi.astype(np.float32)).astype(np.float16)
+        out[b, ok, :half] = fp16_fma(lv, c_lo, ls)
+        out[b, ok, half:] = fp16_fma(rv, c_hi, rs)
     return out
 
 

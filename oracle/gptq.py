@@ -160,15 +160,25 @@ def act_order_perm(g_idx: np.ndarray, groups: int) -> np.ndarray:
     return perm
 
 
-def gemm_ref(x: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """Wide-accumulated product of fp16 activations and the fp16 weight.
+class WideWeight:
+    """An fp16 weight held once in float64, for checkers that multiply the
+    same weight many times (:func:`gemm_ref` then skips its widening)."""
+
+    def __init__(self, w: np.ndarray) -> None:
+        self.w16 = np.asarray(w, dtype=np.float16)
+        self.w64 = self.w16.astype(np.float64)
+
+
+def gemm_ref(x: np.ndarray, w) -> np.ndarray:
+    """Wide-accumulated product of fp16 activations and the fp16 weight
+    (an array or a :class:`WideWeight`).
 
     Returns float64 [M, N]; every product of two fp16 values is exact in
     float64 and the sum is far more accurate than the fp32 accumulation the
     tolerance is stated against.
     """
-    return np.asarray(x, dtype=np.float16).astype(np.float64) @ \
-        np.asarray(w, dtype=np.float16).astype(np.float64)
+    w64 = w.w64 if isinstance(w, WideWeight) else np.asarray(w, dtype=np.float16).astype(np.float64)
+    return np.asarray(x, dtype=np.float16).astype(np.float64) @ w64
 
 
 def forward(x: np.ndarray, qweight: np.ndarray, qzeros: np.ndarray,

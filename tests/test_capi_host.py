@@ -78,6 +78,23 @@ def test_shape_validation_codes():
                              None, 64, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
 
 
+def test_decode_rejects_rows_beyond_32bit_offsets():
+    """The register-fed decode kernel addresses the rows of x with 32-bit
+    element offsets: a forced decode call whose rows span 2^31 elements or
+    more is refused before anything reaches a device (the fake, aligned
+    addresses are never dereferenced); AUTO sends such calls to the prefill
+    kernel instead."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    wide = (1 << 31) + 8  # (m - 1) * ldx alone exceeds INT32_MAX at m = 2
+    assert lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 2, 4096, 4096, 128, fake, wide, fake,
+                             fake, fake, None, None, fake, 4096, None, 0,
+                             None) == _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_gemm_path(_lib.DW4_PATH_DECODE, 0, 64, 4096, 4096, 128, fake,
+                             ((1 << 31) // 63 + 8) & ~7, fake, fake, fake, None, None, fake, 4096,
+                             None, 0, None) == _lib.DW4_ERR_UNSUPPORTED
+
+
 def test_stage_entry_points_validate_before_launch():
     lib = _lib.load()
     fake = 1 << 20  # 16-byte aligned non-null address; never dereferenced on these paths
@@ -266,3 +283,24 @@ def test_synthetic_act_order_groups_uniform():
     counts = torch.bincount(lay.g_idx.long(), minlength=8)
     assert torch.all(counts == 128)
     assert not torch.equal(lay.g_idx, torch.arange(1024, dtype=torch.int32) // 128)
+
+
+def test_rope_tables_accept_only_unbatched_tables():
+    """[P, hd] and [1, 1, P, hd] tables are flattened to [P, hd]; a table
+    with a leading dimension above 1 (or a bare [hd] row) is refused rather
+    than read as more positions."""
+    from hip_extends.w4a16 import rope_tables
+
+    hd = 8
+    t = torch.arange(5 * hd, dtype=torch.float32).view(5, hd)
+    for shape in ((5, hd), (1, 1, 5, hd)):
+        s16, c16, npos = rope_tables(t.view(shape), t.view(shape), hd)
+        assert npos == 5 and tuple(s16.shape) == (5, hd) and s16.dtype == torch.float16
+        assert torch.equal(s16.float(), t)
+    batched = torch.zeros(2, 1, 5, hd)
+    with pytest.raises(ValueError, match="leading dimension"):
+        rope_tables(batched, batched, hd)
+    with pytest.raises(ValueError):
+        rope_tables(torch.zeros(hd), torch.zeros(hd), hd)
+    with pytest.raises(ValueError):
+        rope_tables(torch.zeros(5, hd), torch.zeros(5, hd), 2 * hd)

@@ -106,6 +106,14 @@ CASES = [
     ([300, 41], 32, 4, 128, 16, True),           # 8 per kv head, ALiBi
     ([1500, 2049, 3], 4, 4, 128, 32, False),     # partitions of 512 tokens
     ([33, 90], 6, 3, 256, 16, False),
+    # head sizes that are not multiples of 64: some lanes hold no last key
+    # slice or value dim
+    ([1, 37, 600], 8, 8, 80, 16, False),
+    ([70, 513], 8, 2, 80, 32, True),
+    ([1, 129, 40], 12, 12, 96, 16, False),
+    ([260, 17], 16, 2, 96, 32, False),
+    ([3, 100, 1100], 8, 1, 112, 16, False),
+    ([45, 64], 4, 4, 112, 32, True),
 ]
 
 
@@ -171,8 +179,11 @@ def test_attention_statuses(hip_device):
     lib = _lib.load()
     sz = ctypes.c_size_t(0)
     say("paged attention statuses")
-    assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 96, 16, 100, ctypes.byref(sz)) == \
-        _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 72, 16, 100, ctypes.byref(sz)) == \
+        _lib.DW4_ERR_UNSUPPORTED  # head size not served
+    for hs in (64, 80, 96, 112, 128, 256):
+        assert lib.dw4_paged_attention_workspace_size(2, 8, 8, hs, 16, 100,
+                                                      ctypes.byref(sz)) == _lib.DW4_OK
     assert lib.dw4_paged_attention_workspace_size(2, 36, 4, 128, 16, 100, ctypes.byref(sz)) == \
         _lib.DW4_ERR_UNSUPPORTED  # 9 query heads per kv head
     assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 128, 8, 100, ctypes.byref(sz)) == \

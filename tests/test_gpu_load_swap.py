@@ -11,6 +11,11 @@ make_quant_decoder_linears_from_files, and then:
 * a layer moved to host memory refuses products, and after moving back
   gives bit-identical products with no repack, with q/k/v (and gate/up)
   again sharing one act-order permutation tensor.
+The Marlin-path load (the reference's default backend,
+``operators/assemble/decoders/real_loader_marlin.py:17-91``) reads the same
+files of symmetric checkpoints, merges q/k/v and gate/up, repacks and
+allocates the dense cache; the merged products, the twin bytes and the swap
+are checked the same way.
 Every case prints its name before touching the GPU.
 """
 from __future__ import annotations
@@ -23,9 +28,12 @@ import torch
 from safetensors.torch import save_file
 
 from gptq_synth import GPTQLayer, make_layer, make_x
+from hip_extends.marlin import MarlinTuningParams
 from hip_extends.w4a16 import TuningParams
-from operators.core.linear.loader import make_quant_decoder_linears_from_files
-from operators.core.linear.memory import CacheV2MemoryModel, QuantLinearMakerMemoryModel
+from operators.core.linear.loader import (make_marlin_decoder_linears_from_files,
+                                          make_quant_decoder_linears_from_files)
+from operators.core.linear.memory import (CacheV2MemoryModel, MarlinQuantLinearMakerMemoryModel,
+                                          QuantLinearMakerMemoryModel)
 from operators.core.memory.static import MemoryModule, MemoryTensor
 from oracle import gptq
 
@@ -40,7 +48,7 @@ def say(msg: str) -> None:
     sys.stdout.flush()
 
 
-def _layer_file(path, seed: int, act: bool):
+def _layer_file(path, seed: int, act: bool, symmetric: bool = False):
     """One layer's tensors under the reference's key names; returns the
     oracle's dequantised weight of every projection."""
     shapes = {"self_attn.q_proj": (HIDDEN, HIDDEN), "self_attn.k_proj": (HIDDEN, HIDDEN),
@@ -50,13 +58,14 @@ def _layer_file(path, seed: int, act: bool):
     state, dense = {}, {}
     shared = {}
     for i, (name, (k, n)) in enumerate(shapes.items()):
-        lay = make_layer(k, n, 128, seed=seed + i, act_order=act)
+        lay = make_layer(k, n, 128, seed=seed + i, act_order=act, symmetric=symmetric)
         # q/k/v and gate/up are quantised against one input: equal g_idx
         share_key = "qkv" if name[-6:] in ("q_proj", "k_proj", "v_proj") else \
             "gu" if name.endswith(("gate_proj", "up_proj")) else None
         if act and share_key is not None:
             g_idx = shared.setdefault(share_key, lay.g_idx)
-            lay = GPTQLayer(k, n, 128, lay.qweight, lay.qzeros, lay.scales, g_idx, True, False)
+            lay = GPTQLayer(k, n, 128, lay.qweight, lay.qzeros, lay.scales, g_idx, True,
+                            symmetric)
         for field in ("qweight", "qzeros", "scales", "g_idx"):
             state[f"{name}.{field}"] = getattr(lay, field).contiguous().clone()
         state[f"{name}.bias"] = torch.zeros(n, dtype=torch.float16)
@@ -159,3 +168,95 @@ def test_load_twin_and_swap(hip_device, tmp_path, act):
             torch.cuda.synchronize()
             assert torch.equal(y, before[(li, name)]), (li, name)
     assert _device_bytes(layers, cache) == _twin_bytes(2, act, 64)
+
+
+MERGED = {"self_attn.qkv_proj": ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
+          "self_attn.o_proj": ("self_attn.o_proj",),
+          "mlp.gate_up_proj": ("mlp.gate_proj", "mlp.up_proj"),
+          "mlp.down_proj": ("mlp.down_proj",)}
+
+
+def _marlin_twin_bytes(n_layers: int, act: bool) -> int:
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    maker = MarlinQuantLinearMakerMemoryModel(128, act, workspace_elements=4 * cus)
+    root = MemoryModule()
+    mods = []
+    for i in range(n_layers):
+        q, k, v, o = (maker.make_linear(HIDDEN, HIDDEN) for _ in range(4))
+        gate, up = maker.make_linear(HIDDEN, INTER), maker.make_linear(HIDDEN, INTER)
+        down = maker.make_linear(INTER, HIDDEN)
+        mods += [maker.merge([q, k, v]), o, maker.merge([gate, up]), down]
+        setattr(root, f"norm_in_{i}", MemoryTensor((HIDDEN,), torch.float16))
+        setattr(root, f"norm_post_{i}", MemoryTensor((HIDDEN,), torch.float16))
+    maker.post_init()
+    root.mount_list(mods, "proj")
+    root.dense_cache = maker.dense_cache
+    return root.memory
+
+
+def _marlin_device_bytes(layers, cache) -> int:
+    seen = {}
+    for layer in layers:
+        for t in layer.buffers():
+            if t.numel():
+                seen[t.data_ptr()] = t.numel() * t.element_size()
+    for t in (cache.weight(1, 1), cache.workspace):
+        seen[t.data_ptr()] = t.untyped_storage().nbytes()
+    return sum(seen.values())
+
+
+@pytest.mark.parametrize("act", [False, True], ids=["plain", "act_order"])
+def test_marlin_load_merge_twin_and_swap(hip_device, tmp_path, act):
+    files, denses = [], []
+    for i in range(2):
+        f = tmp_path / f"layer_{i}.safetensors"
+        d, _ = _layer_file(f, 900 + 10 * i, act, symmetric=True)
+        files.append(str(f))
+        denses.append(d)
+    say(f"marlin load 2 layers act={act}")
+    layers, cache, maker = make_marlin_decoder_linears_from_files(
+        HIDDEN, INTER, 128, act, hip_device, files, MarlinTuningParams())
+    torch.cuda.synchronize()
+    assert len(maker.quant_linears) == 2 * 4
+    for layer in layers:
+        assert layer.self_attn.q_proj is None and layer.mlp.gate_proj is None
+        assert sorted(layer.projections()) == sorted(MERGED)
+
+    xs = {k: make_x(5, k, seed=91 + k) for k in (HIDDEN, INTER)}
+    before = {}
+    for li, layer in enumerate(layers):
+        for name, proj in layer.projections().items():
+            say(f"marlin forward layer {li} {name}")
+            x = xs[proj.infeatures]
+            y = proj(x.to(hip_device))
+            torch.cuda.synchronize()
+            w = np.concatenate([denses[li][part] for part in MERGED[name]], axis=1)
+            assert y.shape == (5, w.shape[1])
+            ref = x.numpy().astype(np.float64) @ w.astype(np.float64)
+            ok, worst = gptq.within_tolerance(y.float().cpu().numpy(), ref, TOL)
+            assert ok, f"layer {li} {name}: worst error ratio {worst:.3f}"
+            before[(li, name)] = y.clone()
+
+    say("marlin memory twin")
+    assert _marlin_device_bytes(layers, cache) == _marlin_twin_bytes(2, act)
+
+    say("marlin swap layer 0 out")
+    qkv = layers[0].self_attn.qkv_proj
+    packed = qkv.qweight.clone()
+    layers[0].to("cpu")
+    torch.cuda.synchronize()
+    assert qkv.qweight.device.type == "cpu" and qkv.q4_matrix.qweight.device.type == "cpu"
+    with pytest.raises(RuntimeError):
+        qkv(xs[HIDDEN].to(hip_device))
+    say("marlin swap layer 0 in")
+    layers[0].to(hip_device)
+    torch.cuda.synchronize()
+    assert qkv.q4_matrix.qweight.data_ptr() == qkv.qweight.data_ptr()
+    assert torch.equal(qkv.qweight, packed)  # the packed words, not a second repack
+    for li, layer in enumerate(layers):
+        for name, proj in layer.projections().items():
+            say(f"marlin forward after swap layer {li} {name}")
+            y = proj(xs[proj.infeatures].to(hip_device))
+            torch.cuda.synchronize()
+            assert torch.equal(y, before[(li, name)]), (li, name)
+    assert _marlin_device_bytes(layers, cache) == _marlin_twin_bytes(2, act)

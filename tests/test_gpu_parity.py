@@ -403,24 +403,31 @@ def test_prefill_128_row_tiles_partial(hip_device, k, n, m, g, act):
         check_tol(y, gptq.gemm_ref(x.numpy(), w), f"{k}x{n} M={m} split {split}")
 
 
-def test_prefill_bias_lds_streamed_tiles(hip_device):
-    """Bias in the LDS-streamed kernel's epilogues: the 32 x 128 tiles (M=200,
-    256 at K=4096, a partial last column tile), 64 x 256 with K splits (the
-    bias added by the reduce) and unsplit, against the oracle plus bias."""
-    k, n = 4096, 1040
-    lay, w = oracle_w(k, n, 128, 6060, False, False)
+@pytest.mark.parametrize("k,n,m", [(4096, 1040, 200), (4096, 1040, 256), (11008, 1040, 200),
+                                   (4096, 1040, 600), (2048, 4112, 2000)],
+                         ids=["32x128_M200", "32x128_M256", "64x256_K11008_M200",
+                              "128x128_M600", "128x256_M2000"])
+def test_prefill_bias_lds_streamed_tiles(hip_device, k, n, m):
+    """Bias in the LDS-streamed kernel's epilogues, unsplit (split 1: the
+    tile's own epilogue adds it) and split along K (automatic and 2: the
+    reduce adds it), against the oracle plus bias.  The planner's tiles for
+    these shapes: the 4-wave 32 x 128 workgroups at K = 4096 and M <= 256
+    (a partial last column tile at N = 1040), the 8-wave 64 x 256 at
+    K = 11008 and M = 200 (K beyond 4096 keeps the 8-wave tiles), 128 x 128
+    at M = 600 (above 512 rows; one round of 45 tiles) and 128 x 256 at
+    M = 2000, N = 4112 (two rounds against three for 128 x 128)."""
+    lay, w = oracle_w(k, n, 128, 6060 + m, False, False)
     q4 = build(lay, hip_device)
     bias = (torch.randn(n, generator=torch.Generator().manual_seed(6)) * 0.5).half()
     bd = bias.to(hip_device)
-    for m in (200, 256):
-        for split in (0, 1, 2):
-            say(f"prefill bias {k}x{n} M={m} split={split}")
-            q4.tuning_params = TuningParams(PREFILL_SPLIT_K=split)
-            x = make_x(m, k, seed=m + 606)
-            y = q4.matmul(x.to(hip_device), bias=bd, path=_lib.DW4_PATH_PREFILL)
-            torch.cuda.synchronize()
-            ref = gptq.gemm_ref(x.numpy(), w) + bias.float().numpy()[None, :]
-            check_tol(y, ref, f"bias M={m} split {split}")
+    for split in (0, 1, 2):
+        say(f"prefill bias {k}x{n} M={m} split={split}")
+        q4.tuning_params = TuningParams(PREFILL_SPLIT_K=split)
+        x = make_x(m, k, seed=m + 606)
+        y = q4.matmul(x.to(hip_device), bias=bd, path=_lib.DW4_PATH_PREFILL)
+        torch.cuda.synchronize()
+        ref = gptq.gemm_ref(x.numpy(), w) + bias.float().numpy()[None, :]
+        check_tol(y, ref, f"bias {k}x{n} M={m} split {split}")
 
 
 def test_shared_workspace_across_shapes(hip_device):

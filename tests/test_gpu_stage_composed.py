@@ -28,13 +28,21 @@ fp32-accumulated value (GEMM, attention, SiLU) rounds to the other fp16
 neighbour of the oracle's float64 value -- one unit in the 11th bit (about
 5e-4 of the element).  Those unit differences enter the next op as input
 noise of the same relative size, and each of the two layers adds its own;
-the residual stream carries them unscaled.  Over 2 layers and the 5 steps
+the residual stream carries them unscaled.  Over the layers and steps
 here (whose KV entries are written by the trajectory itself) that stays an
 order of magnitude below 2e-2; the measured worst ratio is printed.
+
+Two cases: ``short`` (2 layers, per-sequence contexts of 8-45 tokens, so the
+5 steps cross the 16-, 32- and 48-token block boundaries) and ``c5``, config
+5's own shapes: 4 of the stage's 8 layers (the oracle's run time), batch 8,
+contexts of 496-512 tokens at step 0 (so the steps cross the 512-token block
+boundary), 16-token blocks, 32 heads x 128, one eager step and 4 graph
+replays, every step checked.
 """
 from __future__ import annotations
 
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -54,12 +62,13 @@ from oracle import gptq, stage
 pytestmark = pytest.mark.gpu
 
 HIDDEN, INTER, HEADS, HD = 4096, 11008, 32, 128
-LAYERS, BATCH, STEPS, BS = 2, 8, 5, 16
+BATCH, STEPS, BS = 8, 5, 16
 EPS = 1e-5
 TOL = 2e-2
-# per-sequence context before step 0: partial and full blocks, and steps
-# that cross a block boundary (16, 32, 48)
-CTX0 = np.array([29, 30, 17, 45, 31, 8, 40, 13], np.int32)
+# (layers, per-sequence context before step 0): partial and full blocks and
+# steps that cross block boundaries (16, 32, 48; 512)
+CASES = {"short": (2, np.array([29, 30, 17, 45, 31, 8, 40, 13], np.int32)),
+         "c5": (4, np.array([512, 509, 511, 496, 500, 505, 508, 510], np.int32))}
 PROJ = (("q_proj", HIDDEN, HIDDEN), ("k_proj", HIDDEN, HIDDEN), ("v_proj", HIDDEN, HIDDEN),
         ("o_proj", HIDDEN, HIDDEN), ("gate_proj", HIDDEN, INTER), ("up_proj", HIDDEN, INTER),
         ("down_proj", INTER, HIDDEN))
@@ -70,31 +79,44 @@ def say(msg: str) -> None:
     sys.stdout.flush()
 
 
-def test_composed_stage_graph_replay_matches_oracle(hip_device):
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_composed_stage_graph_replay_matches_oracle(hip_device, case):
     dev = hip_device
     old_bs = flags.BLOCK_SIZE
     flags.BLOCK_SIZE = BS
     try:
-        _run(dev)
+        _run(dev, *CASES[case])
     finally:
         flags.BLOCK_SIZE = old_bs
 
 
-def _run(dev):
-    say(f"composed stage: building {LAYERS} Llama-2-7B layers")
+def _oracle_layer(li: int):
+    """One layer's synthetic GPTQ projections and their oracle weights."""
+    out = []
+    for pi, (name, k, n) in enumerate(PROJ):
+        lay = make_layer(k, n, 128, seed=9000 + 10 * li + pi, scale_mul=0.002, scale_add=2e-4)
+        a = lay.numpy()
+        w = gptq.dequantize(a["qweight"], a["qzeros"], a["scales"], a["g_idx"])
+        out.append((name, k, n, lay, gptq.WideWeight(w)))
+    return out
+
+
+def _run(dev, LAYERS, CTX0):
+    say(f"composed stage: building {LAYERS} Llama-2-7B layers, contexts {CTX0.tolist()}")
     cache = CacheV2(dev)
     tp = TuningParams(MAX_M=BATCH)
     mats, w_ref = [], []
-    for li in range(LAYERS):
+    with ThreadPoolExecutor(max_workers=min(LAYERS, 8)) as pool:
+        built = list(pool.map(_oracle_layer, range(LAYERS)))
+    for layer in built:
         lm, lw = {}, {}
-        for pi, (name, k, n) in enumerate(PROJ):
-            lay = make_layer(k, n, 128, seed=9000 + 10 * li + pi, scale_mul=0.002, scale_add=2e-4)
-            a = lay.numpy()
-            lw[name] = gptq.dequantize(a["qweight"], a["qzeros"], a["scales"], a["g_idx"])
+        for name, k, n, lay, ww in layer:
+            lw[name] = ww
             d = lay.to(dev)
             lm[name] = Q4MatrixV2(d.qweight, d.qzeros, d.scales, k, n, None, False, tp, cache)
         mats.append(lm)
         w_ref.append(lw)
+    del built
     cache.init_cache()
     rng = np.random.default_rng(77)
     norm_in = [(1.0 + 0.1 * rng.standard_normal(HIDDEN)).astype(np.float16) for _ in range(LAYERS)]

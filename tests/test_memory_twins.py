@@ -14,7 +14,8 @@ import torch
 from hip_extends import _lib
 from hip_extends.w4a16 import TuningParams
 from operators.core.linear.memory import (CacheV2MemoryModel, MarlinQuantLinearMakerMemoryModel,
-                                          QuantLinearMakerMemoryModel, QuantLinearMemoryModel)
+                                          QuantLinearMakerMemoryModel, QuantLinearMemoryModel,
+                                          W4A16LibraryMemoryModel)
 from operators.core.linear.real_quant import QuantLinear
 from operators.core.memory.static import MemoryModule, MemoryTensor
 
@@ -104,3 +105,29 @@ def test_memory_tensor_basics():
     m.c = MemoryTensor((2,), torch.int32)
     assert m.memory == 38
     assert [n for n, _ in m.named_parameters()] == ["a", "b", "c"]
+
+
+def test_library_twin_counts_the_noalloc_scratch():
+    """The per-GPU static array of dw4_gemm_noalloc (the header's
+    DW4_NOALLOC_SCRATCH_BYTES) is in the library twin, counted once when a
+    device plan mounts it beside a decoder group's twins."""
+    import os
+    import re
+
+    header = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                               "include", "drofell_w4a16.h")).read()
+    shift = int(re.search(r"#define DW4_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << 20\)",
+                          header).group(1))
+    assert _lib.NOALLOC_SCRATCH_BYTES == shift << 20
+    lib_twin = W4A16LibraryMemoryModel()
+    assert lib_twin.memory == _lib.NOALLOC_SCRATCH_BYTES
+    maker = QuantLinearMakerMemoryModel(128, False)
+    lin = maker.make_linear(4096, 4096)
+    cache = CacheV2MemoryModel()
+    maker.post_init(TuningParams(MAX_M=64), cache)
+    cache.init_cache()
+    device = MemoryModule()
+    device.library = lib_twin
+    device.proj = lin
+    device.workspace = cache.workspace  # the linear's twin holds it already: counted once
+    assert device.memory == lib_twin.memory + lin.memory

@@ -675,3 +675,13 @@ def test_dequantize_bf16_is_bf16_of_fp16_weight():
     wb = gptq.dequantize_bf16(qweight, qzeros, scales, g)
     rel = np.abs(gptq.bf16_to_float(wb) - w.astype(np.float32)) / np.maximum(np.abs(w.astype(np.float32)), 1e-30)
     assert np.all(rel <= 2.0 ** -8)  # one bf16 rounding (8 significant bits) of the fp16 value
+
+
+def test_gemm_ref_wide_weight_is_the_same_product():
+    """A weight widened once (WideWeight) gives gemm_ref's product bit for bit."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 64)).astype(np.float16)
+    w = (rng.standard_normal((64, 48)) * 0.1).astype(np.float16)
+    ww = gptq.WideWeight(w)
+    assert np.array_equal(gptq.gemm_ref(x, ww), gptq.gemm_ref(x, w))
+    assert ww.w64.dtype == np.float64 and np.array_equal(ww.w16, w)

@@ -176,6 +176,34 @@ def test_fp16_round_matches_numpy():
     assert A.fp16_round(Fraction(2051, 2)) == np.float16(1026.0)
 
 
+def test_fp16_fma_vector_form_matches_exact_scalar_form():
+    """The vector fma (float64 TwoSum, then one rounding) against the
+    Fraction-based scalar one on random fp16 triples over every exponent
+    range, subnormals, signed zeros, exact ties (3 * 341.5 = 1024.5 lies
+    halfway between fp16 neighbours) and overflow; a planted double rounding
+    (via float32) must disagree somewhere."""
+    rng = np.random.default_rng(11)
+    n = 4000
+    bits = rng.integers(0, 1 << 16, size=(3, n), dtype=np.uint32).astype(np.uint16)
+    a, b, c = (v.view(np.float16) for v in bits)
+    fin = np.isfinite(a) & np.isfinite(b) & np.isfinite(c)
+    a, b, c = a[fin], b[fin], c[fin]
+    moderate = (rng.standard_normal((3, 2000)) * 4).astype(np.float16)
+    special = np.array([[3, 3, -3, 0, -0.0, 0, 2 ** -24, 2 ** -14, 65504, 255.9],
+                        [341.5, 341.5, 341.5, 5, 1, -0.0, 2 ** -24, 2 ** -10, 2, 256.1],
+                        [0, 2 ** -24, -(2 ** -24), -0.0, -0.0, -0.0, 1, 0, 65504, -1]],
+                       dtype=np.float16)
+    a = np.concatenate([a, moderate[0], special[0]])
+    b = np.concatenate([b, moderate[1], special[1]])
+    c = np.concatenate([c, moderate[2], special[2]])
+    got = A.fp16_fma(a, b, c)
+    want = np.array([A._fp16_fma(x, y, z) for x, y, z in zip(a, b, c)], np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert A.fp16_fma(np.float16(3), np.float16(341.5), np.float16(0)) == np.float16(1024)
+    sloppy = (a.astype(np.float32) * b.astype(np.float32) + c.astype(np.float32)).astype(np.float16)
+    assert not np.array_equal(sloppy.view(np.uint16), want.view(np.uint16))
+
+
 def test_rope_closed_forms_and_mistakes():
     rng = np.random.default_rng(8)
     hd, heads = 16, 2

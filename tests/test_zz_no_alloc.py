@@ -6,7 +6,11 @@ library's fixed per-GPU scratch array instead of a caller workspace, so its
 output must equal dw4_gemm's bit for bit.  Two calls in a row, the second
 smaller, check that what the first left in the shared array does not leak
 into the second; a call needing more than the array is refused before any
-launch.
+launch.  The register-fed prefill kernel's in-kernel split-K (M of 33-128
+rows) keeps per-tile arrival counters at the head of the array, which every
+call must leave at zero: two such calls in a row check that.  A call
+captured into a HIP graph (after one eager call has set the array up on the
+device) replays to the same bits.
 """
 from __future__ import annotations
 
@@ -62,9 +66,10 @@ def _both(q4, m, seed):
 
 @pytest.mark.parametrize("act", [False, True], ids=["plain", "act"])
 def test_noalloc_matches_gemm_two_calls(hip_device, act):
-    """First call: M=256 on 8192x4096 (split-K prefill: partial planes and
-    arrival counters in the scratch; act-order also gathers x there).  Second
-    call, smaller: M=40 on 4096x2048, then M=1 decode."""
+    """First call: M=256 on 8192x4096 (the LDS-streamed prefill kernel split
+    over K: fp32 partial planes in the scratch, summed by a second kernel;
+    act-order also gathers x there).  Second call, smaller: M=40 on
+    4096x2048, then M=1 decode."""
     big = _matrix(hip_device, 8192, 4096, act, 61)
     small = _matrix(hip_device, 4096, 2048, act, 62)
     assert _lib.workspace_size(256, 8192, 4096, 128, False) > 0  # the scratch is really used
@@ -73,6 +78,50 @@ def test_noalloc_matches_gemm_two_calls(hip_device, act):
         y_ref, y = _both(q4, m, seed=m + 3 * act)
         assert not torch.isnan(y).any()
         assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), f"M={m}"
+
+
+def test_noalloc_split_counters_return_to_zero(hip_device):
+    """M=96 on 4096x4096 runs the register-fed prefill kernel split over K,
+    whose last-arriving split of each tile sums the partials and resets that
+    tile's arrival counter at the head of the scratch.  Two calls in a row
+    (then one with M=72) equal dw4_gemm bit for bit: a counter left non-zero
+    by the first call would make the second call's sums start early."""
+    q4 = _matrix(hip_device, 4096, 4096, False, 63)
+    assert _lib.workspace_size(96, 4096, 4096, 128, False) > 0  # split: counters in use
+    for m in (96, 96, 72):
+        say(f"noalloc vs gemm split counters 4096x4096 M={m}")
+        y_ref, y = _both(q4, m, seed=m)
+        assert not torch.isnan(y).any()
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), f"M={m}"
+
+
+def test_noalloc_captured_in_graph(hip_device):
+    """One eager call sets the scratch up on the device (address lookup and
+    counter clear); a call captured into a HIP graph then replays three
+    times, with other device work between the replays, each equal to
+    dw4_gemm bit for bit."""
+    lib = _lib.load()
+    q4 = _matrix(hip_device, 4096, 4096, False, 64)
+    k = n = 4096
+    m = 96
+    say("noalloc graph capture 4096x4096 M=96")
+    y_ref, _ = _both(q4, m, seed=5)  # eager: also the first use on the device
+    x = make_x(m, k, seed=5).to(hip_device)
+    y = torch.zeros(m, n, dtype=torch.float16, device=hip_device)
+    side = torch.cuda.Stream(device=hip_device)
+    side.wait_stream(torch.cuda.current_stream(hip_device))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        st = lib.dw4_gemm_noalloc(m, k, n, 128, x.data_ptr(), k, q4.qweight.data_ptr(),
+                                  q4.qzeros.data_ptr(), q4.scales.data_ptr(), None, None,
+                                  y.data_ptr(), n, side.cuda_stream)
+        assert st == _lib.DW4_OK, _lib.strerror(st)
+    for r in range(3):
+        y.fill_(float("nan"))
+        _ = torch.randn(1 << 20, device=hip_device).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), f"replay {r}"
 
 
 def test_noalloc_refuses_calls_beyond_its_scratch(hip_device):
