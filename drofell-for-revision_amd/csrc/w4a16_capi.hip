@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -972,3 +973,172 @@ extern "C" int dw4_gemm_noalloc(int m, int k, int n, int group_size, const uint1
                   packed_scales, perm, bias, y, ldy, nullptr, 0, ws, DW4_NOALLOC_SCRATCH_BYTES,
                   stream);
 }
+
+// ---------------------------------------------------------------------------
+// Decode chain
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Span {
+  uintptr_t lo = 0, hi = 0;  // [lo, hi) bytes; empty when lo == hi
+  bool hits(const Span& o) const { return lo < o.hi && o.lo < hi; }
+};
+
+Span span_of(const void* p, int m, int64_t ld, int cols) {
+  Span r;
+  if (p == nullptr || m <= 0) return r;
+  r.lo = reinterpret_cast<uintptr_t>(p);
+  r.hi = r.lo + ((size_t)(m - 1) * (size_t)ld + (size_t)cols) * sizeof(uint16_t);
+  return r;
+}
+
+int check_chain_link(const dw4_chain_link& l, int i, int m) {
+  int st = check_shape(l.k, l.n, l.group_size);
+  if (st != DW4_OK) return st;
+  if (l.group_size % kChunkK != 0 || l.perm != nullptr || l.k > dw4::kChainMaxK ||
+      l.n > 32768)
+    return DW4_ERR_UNSUPPORTED;
+  if (!l.x || !l.packed_qweight || !l.packed_zeros || !l.packed_scales || !l.y)
+    return DW4_ERR_INVALID_ARG;
+  if (l.ldx < l.k || l.ldy < l.n || (l.residual && l.ldres < l.n)) return DW4_ERR_INVALID_ARG;
+  if (l.after < -1 || l.after >= i) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(l.x) || l.ldx % 8 != 0 || !aligned16(l.packed_qweight)) return DW4_ERR_MISALIGNED;
+  // the activation rows are read through one buffer resource (32-bit offsets)
+  if ((int64_t)(m - 1) * l.ldx * 2 + (int64_t)l.k * 2 > (int64_t)INT32_MAX)
+    return DW4_ERR_UNSUPPORTED;
+  return DW4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dw4_chain_buffer_size(int count, size_t* bytes) {
+  if (count < 1 || count > (1 << 16) || bytes == nullptr) return DW4_ERR_INVALID_ARG;
+  *bytes = dw4::chain_buffer_bytes(count);
+  return DW4_OK;
+}
+
+int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain,
+                      size_t chain_bytes, dw4_chain_plan* plan) {
+  if (count < 1 || count > (1 << 16) || links == nullptr || plan == nullptr)
+    return DW4_ERR_INVALID_ARG;
+  if (m < 1 || m > dw4::kChainMaxM) return DW4_ERR_UNSUPPORTED;
+  for (int i = 0; i < count; ++i) {
+    const int st = check_chain_link(links[i], i, m);
+    if (st != DW4_OK) return st;
+  }
+  // Every pair of links that share a buffer with at least one of them
+  // writing it must be ordered by `after`; within a link the output must not
+  // overlap its activations or bias, and the residual is the output itself
+  // (same stride) or elsewhere.
+  std::vector<Span> w(count), xr(count), rr(count), br(count);
+  for (int i = 0; i < count; ++i) {
+    const dw4_chain_link& l = links[i];
+    w[i] = span_of(l.y, m, l.ldy, l.n);
+    xr[i] = span_of(l.x, m, l.ldx, l.k);
+    rr[i] = span_of(l.residual, m, l.ldres, l.n);
+    br[i] = span_of(l.bias, 1, l.n, l.n);
+    if (w[i].hits(xr[i]) || w[i].hits(br[i])) return DW4_ERR_INVALID_ARG;
+    if (w[i].hits(rr[i]) && !(l.residual == l.y && l.ldres == l.ldy)) return DW4_ERR_INVALID_ARG;
+  }
+  for (int b = 1; b < count; ++b)
+    for (int a = 0; a < b; ++a) {
+      const bool conflict = w[a].hits(w[b]) || w[a].hits(xr[b]) || w[a].hits(rr[b]) ||
+                            w[a].hits(br[b]) || w[b].hits(xr[a]) || w[b].hits(rr[a]) ||
+                            w[b].hits(br[a]);
+      if (conflict && links[b].after < a) return DW4_ERR_INVALID_ARG;
+    }
+  size_t need = dw4::chain_buffer_bytes(count);
+  if (chain == nullptr || chain_bytes < need) return DW4_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(chain) & 255u) != 0) return DW4_ERR_MISALIGNED;
+
+  dw4::ChainPlan p{};
+  p.count = count;
+  p.m = m;
+  p.workgroups = std::min(cu_count(), dw4::kChainMaxWorkgroups);
+  p.max_k = 0;
+  p.max_strips = 1;
+  for (int i = 0; i < count; ++i) {
+    p.max_k = std::max(p.max_k, links[i].k);
+    const int strips = links[i].n / kStripN;
+    p.max_strips = std::max(p.max_strips, (strips + p.workgroups - 1) / p.workgroups);
+  }
+  if (!dw4::plan_chain(p)) return DW4_ERR_UNSUPPORTED;
+
+  std::vector<unsigned char> host(need, 0);
+  dw4::ChainHeader* hdr = reinterpret_cast<dw4::ChainHeader*>(host.data());
+  hdr->count = count;
+  hdr->M = m;
+  hdr->workgroups = p.workgroups;
+  int64_t strips_before = 0;
+  for (int i = 0; i < count; ++i) {
+    const dw4_chain_link& l = links[i];
+    dw4::ChainLinkDev d{};
+    d.pq = reinterpret_cast<const uint32_t*>(l.packed_qweight);
+    d.pz = reinterpret_cast<const uint32_t*>(l.packed_zeros);
+    d.ps32 = reinterpret_cast<const uint32_t*>(l.packed_scales);
+    d.x = l.x;
+    d.bias = l.bias;
+    d.res = l.residual;
+    d.y = l.y;
+    d.ldx = l.ldx;
+    d.ldres = l.ldres;
+    d.ldy = l.ldy;
+    d.K = l.k;
+    d.N = l.n;
+    d.G = l.k / l.group_size;
+    const int cpg = l.group_size / kChunkK;  // chunks per group
+    d.gmag = cpg <= 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)cpg - 1) / (uint64_t)cpg);
+    const int kc = l.k / kChunkK;
+    d.kcmag = kc <= 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)kc - 1) / (uint64_t)kc);
+    d.after = l.after;
+    d.flags = 0;
+    if (i > 0) {
+      const dw4_chain_link& q = links[i - 1];
+      if (q.x == l.x && q.ldx == l.ldx && q.k == l.k && q.after == l.after)
+        d.flags |= dw4::kChainSameX;
+    }
+    d.rot = (int)(strips_before % p.workgroups);
+    strips_before += l.n / kStripN;
+    std::memcpy(host.data() + dw4::kChainHeadBytes + (size_t)i * dw4::kChainLinkBytes, &d,
+                sizeof(d));
+  }
+  if (hipMemcpy(chain, host.data(), need, hipMemcpyHostToDevice) != hipSuccess)
+    return DW4_ERR_DEVICE;
+  plan->count = p.count;
+  plan->m = p.m;
+  plan->workgroups = p.workgroups;
+  plan->waves = p.waves;
+  plan->ring = p.ring;
+  plan->max_k = p.max_k;
+  plan->max_strips = p.max_strips;
+  plan->smem_bytes = p.smem;
+  return DW4_OK;
+}
+
+int dw4_gemm_chain(const dw4_chain_plan* plan, void* chain, void* stream) {
+  if (plan == nullptr || chain == nullptr || plan->count < 1 || plan->m < 1 ||
+      plan->m > dw4::kChainMaxM || plan->workgroups < 1 ||
+      plan->workgroups > dw4::kChainMaxWorkgroups)
+    return DW4_ERR_INVALID_ARG;
+  dw4::ChainPlan p{};
+  p.count = plan->count;
+  p.m = plan->m;
+  p.workgroups = plan->workgroups;
+  p.max_k = plan->max_k;
+  p.max_strips = plan->max_strips;
+  if (!dw4::plan_chain(p) || p.ring != plan->ring || p.smem != plan->smem_bytes)
+    return DW4_ERR_INVALID_ARG;  // not a plan dw4_chain_prepare wrote
+  return status_of(dw4::launch_chain(p, chain, static_cast<hipStream_t>(stream)));
+}
+
+int dw4_chain_timed_out(const void* chain, int* timed_out) {
+  if (chain == nullptr || timed_out == nullptr) return DW4_ERR_INVALID_ARG;
+  dw4::ChainHeader h{};
+  if (hipMemcpy(&h, chain, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return DW4_ERR_DEVICE;
+  *timed_out = h.timed_out != 0;
+  return DW4_OK;
+}
+
+}  // extern "C"

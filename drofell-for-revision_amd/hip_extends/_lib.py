@@ -44,6 +44,28 @@ class Item(ctypes.Structure):
 
 _IP = _c.POINTER(Item)
 
+
+class ChainLink(ctypes.Structure):
+    """``dw4_chain_link``: one projection of a decode chain."""
+
+    _fields_ = [("k", _c.c_int), ("n", _c.c_int), ("group_size", _c.c_int),
+                ("packed_qweight", _P), ("packed_zeros", _P), ("packed_scales", _P),
+                ("perm", _P), ("x", _P), ("ldx", _c.c_int64), ("bias", _P),
+                ("residual", _P), ("ldres", _c.c_int64), ("y", _P), ("ldy", _c.c_int64),
+                ("after", _c.c_int)]
+
+
+class ChainPlan(ctypes.Structure):
+    """``dw4_chain_plan``: filled by dw4_chain_prepare, read by dw4_gemm_chain."""
+
+    _fields_ = [("count", _c.c_int), ("m", _c.c_int), ("workgroups", _c.c_int),
+                ("waves", _c.c_int), ("ring", _c.c_int), ("max_k", _c.c_int),
+                ("max_strips", _c.c_int), ("smem_bytes", _c.c_size_t)]
+
+
+_CLP = _c.POINTER(ChainLink)
+_CPP = _c.POINTER(ChainPlan)
+
 # Every symbol the public header declares, with its ctypes signature.
 SIGNATURES = {
     "dw4_abi_version": (_c.c_int, []),
@@ -96,8 +118,12 @@ SIGNATURES = {
     "dw4_decoder_after_stage": (_c.c_int, [_c.c_int, _P, _c.c_int64, _P, _c.c_int64, _IP, _P,
                                            _c.c_float, _P, _c.c_int64, _IP, _IP, _IP, _P,
                                            _c.c_size_t, _P]),
+    "dw4_chain_buffer_size": (_c.c_int, [_c.c_int, _SZ]),
+    "dw4_chain_prepare": (_c.c_int, [_c.c_int, _CLP, _c.c_int, _P, _c.c_size_t, _CPP]),
+    "dw4_gemm_chain": (_c.c_int, [_CPP, _P, _P]),
+    "dw4_chain_timed_out": (_c.c_int, [_P, _c.POINTER(_c.c_int)]),
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -100,7 +100,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 8
+#define DW4_ABI_VERSION 9
 
 enum {
   DW4_OK = 0,
@@ -413,6 +413,66 @@ int dw4_rope_and_cache(int num_seqs, int num_heads, int num_kv_heads, int head_d
                        int max_blocks_per_seq, const int64_t* key_block_ptrs,
                        const int64_t* value_block_ptrs, int kv_head_stride,
                        int32_t* context_lens_out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode chain: one launch over a list of projections at m <= 4 (no single
+ * reference call: it runs the per-projection q4_matmul_cuda_v2 calls,
+ * cuda_extends/exllama/entry.cpp:221-251, that the layer loop of
+ * operators/assemble/decoders/real_decoders_group.py:106-159 makes for one
+ * decode step, in one kernel).  Every workgroup streams the packed weights of
+ * its share of all links back to back, so the weight stream does not stop at
+ * the dependency points between projections; a link's activations are read
+ * only once the links it depends on are complete on every workgroup.
+ *
+ * Link i: y_i = fp16(fp16(x_i @ W_i) (+ bias_i)) (+ residual_i) with fp32
+ * accumulation, x_i fp16 [m, k] (row stride ldx), y_i fp16 [m, n] (ldy),
+ * residual_i NULL or fp16 [m, n] (ldres; it may be y_i itself).  `after`
+ * is -1 (x_i is ready when the launch starts) or the index of an earlier
+ * link: x_i (and residual_i) are read only after links 0..after have
+ * completed.  Every two links of which one writes a buffer the other reads
+ * or writes must be ordered that way (the later one's `after` at least the
+ * earlier one's index); dw4_chain_prepare refuses a list that is not.
+ * Supported: group_size a multiple of 128, no act-order (perm NULL),
+ * k <= 16384, n <= 32768, m <= 4.  Results are deterministic; the sums run
+ * in another order than dw4_gemm's, so the two agree to the GEMM tolerance,
+ * not bit for bit.
+ *
+ * dw4_chain_prepare validates a list and writes it, with the chain's
+ * progress state, into `chain` (device memory of dw4_chain_buffer_size
+ * bytes, owned by the caller); it copies synchronously and must not be
+ * captured.  dw4_gemm_chain then launches the list as prepared (capturable
+ * and replayable; launches of one chain buffer must not overlap in time).
+ * The pointers in the links are used as given at every launch.  The plan
+ * struct is filled by prepare and only read by the launch.
+ * dw4_chain_timed_out reports (synchronously) whether a launch on this
+ * buffer gave up waiting for a dependency (about 0.2 s; the kernel then
+ * finishes with invalid outputs instead of hanging). */
+typedef struct dw4_chain_link {
+  int k, n, group_size;
+  const int32_t* packed_qweight;
+  const int32_t* packed_zeros;
+  const uint16_t* packed_scales;
+  const int32_t* perm;
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* bias;
+  const uint16_t* residual;
+  int64_t ldres;
+  uint16_t* y;
+  int64_t ldy;
+  int after;
+} dw4_chain_link;
+
+typedef struct dw4_chain_plan {
+  int count, m, workgroups, waves, ring, max_k, max_strips;
+  size_t smem_bytes;
+} dw4_chain_plan;
+
+int dw4_chain_buffer_size(int count, size_t* bytes);
+int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain,
+                      size_t chain_bytes, dw4_chain_plan* plan);
+int dw4_gemm_chain(const dw4_chain_plan* plan, void* chain, void* stream);
+int dw4_chain_timed_out(const void* chain, int* timed_out);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 8
+    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 9
 
 
 def test_strerror_names_every_status():
@@ -304,3 +304,49 @@ def test_rope_tables_accept_only_unbatched_tables():
         rope_tables(torch.zeros(hd), torch.zeros(hd), hd)
     with pytest.raises(ValueError):
         rope_tables(torch.zeros(5, hd), torch.zeros(5, hd), 2 * hd)
+
+
+def test_chain_prepare_validates_before_touching_a_device():
+    """dw4_chain_prepare refuses unsupported links and unordered buffer
+    sharing before any device call (fake, aligned addresses are never
+    dereferenced: every case fails validation or meets the null chain
+    buffer first)."""
+    lib = _lib.load()
+    size = ctypes.c_size_t(0)
+    assert lib.dw4_chain_buffer_size(3, ctypes.byref(size)) == _lib.DW4_OK and size.value > 0
+    assert lib.dw4_chain_buffer_size(0, ctypes.byref(size)) == _lib.DW4_ERR_INVALID_ARG
+    k = n = 4096
+    mat = dict(packed_qweight=1 << 24, packed_zeros=2 << 24, packed_scales=3 << 24)
+    bufs = [(8 + i) << 24 for i in range(8)]
+
+    def link(x, y, after=-1, **kw):
+        fields = dict(k=k, n=n, group_size=128, x=x, ldx=k, y=y, ldy=n, after=after, **mat)
+        fields.update(kw)
+        return _lib.ChainLink(**fields)
+
+    def prepare(links, m=1):
+        arr = (_lib.ChainLink * len(links))(*links)
+        plan = _lib.ChainPlan()
+        return lib.dw4_chain_prepare(len(links), arr, m, None, 0, ctypes.byref(plan))
+
+    ok_chain = [link(bufs[0], bufs[1]), link(bufs[1], bufs[2], after=0)]
+    assert prepare(ok_chain) == _lib.DW4_ERR_WORKSPACE  # valid list, no chain buffer
+    assert prepare(ok_chain, m=5) == _lib.DW4_ERR_UNSUPPORTED
+    # link 1 reads link 0's output without waiting for it
+    assert prepare([link(bufs[0], bufs[1]), link(bufs[1], bufs[2])]) == _lib.DW4_ERR_INVALID_ARG
+    # link 1 overwrites what link 0 reads, unordered
+    assert prepare([link(bufs[0], bufs[1]), link(bufs[2], bufs[0])]) == _lib.DW4_ERR_INVALID_ARG
+    # a link's output overlapping its own input or bias
+    assert prepare([link(bufs[0], bufs[0] + 64)]) == _lib.DW4_ERR_INVALID_ARG
+    assert prepare([link(bufs[0], bufs[1], bias=bufs[1])]) == _lib.DW4_ERR_INVALID_ARG
+    # in-place residual is fine, a shifted one is not
+    assert prepare([link(bufs[0], bufs[1], residual=bufs[1], ldres=n)]) == _lib.DW4_ERR_WORKSPACE
+    assert prepare([link(bufs[0], bufs[1], residual=bufs[1] + 16, ldres=n)]) == \
+        _lib.DW4_ERR_INVALID_ARG
+    # `after` must name an earlier link
+    assert prepare([link(bufs[0], bufs[1], after=0)]) == _lib.DW4_ERR_INVALID_ARG
+    # unsupported forms: act-order, small groups, K beyond 16384
+    assert prepare([link(bufs[0], bufs[1], perm=bufs[5])]) == _lib.DW4_ERR_UNSUPPORTED
+    assert prepare([link(bufs[0], bufs[1], group_size=64)]) == _lib.DW4_ERR_UNSUPPORTED
+    assert prepare([link(bufs[0], bufs[1], k=16512, ldx=16512)]) == _lib.DW4_ERR_UNSUPPORTED
+    assert lib.dw4_gemm_chain(None, None, None) == _lib.DW4_ERR_INVALID_ARG
