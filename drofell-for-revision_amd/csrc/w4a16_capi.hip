@@ -1059,8 +1059,10 @@ int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain
   p.workgroups = std::min(cu_count(), dw4::kChainMaxWorkgroups);
   p.max_k = 0;
   p.max_strips = 1;
+  p.max_groups = 1;
   for (int i = 0; i < count; ++i) {
     p.max_k = std::max(p.max_k, links[i].k);
+    p.max_groups = std::max(p.max_groups, links[i].k / links[i].group_size);
     const int strips = links[i].n / kStripN;
     p.max_strips = std::max(p.max_strips, (strips + p.workgroups - 1) / p.workgroups);
   }
@@ -1099,6 +1101,11 @@ int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain
       if (q.x == l.x && q.ldx == l.ldx && q.k == l.k && q.after == l.after)
         d.flags |= dw4::kChainSameX;
     }
+    // a link's progress is published only when a later link waits for it
+    // (waiting for link a means links 0..a are complete: the latest
+    // published link at or before a carries that)
+    for (int b = i + 1; b < count; ++b)
+      if (links[b].after == i) d.flags |= dw4::kChainPublish;
     d.rot = (int)(strips_before % p.workgroups);
     strips_before += l.n / kStripN;
     std::memcpy(host.data() + dw4::kChainHeadBytes + (size_t)i * dw4::kChainLinkBytes, &d,
@@ -1113,6 +1120,7 @@ int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain
   plan->ring = p.ring;
   plan->max_k = p.max_k;
   plan->max_strips = p.max_strips;
+  plan->max_groups = p.max_groups;
   plan->smem_bytes = p.smem;
   return DW4_OK;
 }
@@ -1128,6 +1136,7 @@ int dw4_gemm_chain(const dw4_chain_plan* plan, void* chain, void* stream) {
   p.workgroups = plan->workgroups;
   p.max_k = plan->max_k;
   p.max_strips = plan->max_strips;
+  p.max_groups = plan->max_groups;
   if (!dw4::plan_chain(p) || p.ring != plan->ring || p.smem != plan->smem_bytes)
     return DW4_ERR_INVALID_ARG;  // not a plan dw4_chain_prepare wrote
   return status_of(dw4::launch_chain(p, chain, static_cast<hipStream_t>(stream)));

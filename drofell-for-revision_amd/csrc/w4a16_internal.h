@@ -403,6 +403,7 @@ constexpr int kChainMaxWorkgroups = 1024;
 constexpr int kChainLinkBytes = 128;
 constexpr int kChainHeadBytes = 256;
 constexpr int kChainSameX = 1;         // link flag: x already in LDS (previous link's x)
+constexpr int kChainPublish = 2;       // link flag: a later link waits for this one
 
 struct ChainLinkDev {
   const uint32_t* pq;
@@ -416,7 +417,7 @@ struct ChainLinkDev {
   int K, N, G;
   uint32_t gmag;   // chunk -> group: g = umulhi(c, gmag) (0: group = chunk)
   int after;       // -1, or: read x once links 0..after are complete everywhere
-  int flags;       // kChainSameX
+  int flags;       // kChainSameX, kChainPublish
   int rot;         // workgroup rotation of the strip ranges, in [0, workgroups)
   uint32_t kcmag;  // ceil(2^32 / (K / 128)) (0 when K = 128)
   unsigned char pad_to_record[kChainLinkBytes - 112];
@@ -441,11 +442,11 @@ inline size_t chain_buffer_bytes(int count) {
 }
 
 struct ChainPlan {
-  int count, m, workgroups, waves, ring, max_k, max_strips;
+  int count, m, workgroups, waves, ring, max_k, max_strips, max_groups;
   size_t smem;
 };
 // LDS bytes of a chain workgroup for a plan's ring depth.
-size_t chain_smem_bytes(int m, int max_k, int max_strips, int waves, int ring);
+size_t chain_smem_bytes(int m, int max_k, int max_strips, int max_groups, int waves, int ring);
 // Picks the ring depth (units in flight per streaming wave) and LDS size.
 bool plan_chain(ChainPlan& p);
 hipError_t launch_chain(const ChainPlan& p, void* chain, hipStream_t stream);

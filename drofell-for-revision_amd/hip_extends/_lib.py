@@ -60,7 +60,8 @@ class ChainPlan(ctypes.Structure):
 
     _fields_ = [("count", _c.c_int), ("m", _c.c_int), ("workgroups", _c.c_int),
                 ("waves", _c.c_int), ("ring", _c.c_int), ("max_k", _c.c_int),
-                ("max_strips", _c.c_int), ("smem_bytes", _c.c_size_t)]
+                ("max_strips", _c.c_int), ("max_groups", _c.c_int),
+                ("smem_bytes", _c.c_size_t)]
 
 
 _CLP = _c.POINTER(ChainLink)

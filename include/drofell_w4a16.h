@@ -464,7 +464,7 @@ typedef struct dw4_chain_link {
 } dw4_chain_link;
 
 typedef struct dw4_chain_plan {
-  int count, m, workgroups, waves, ring, max_k, max_strips;
+  int count, m, workgroups, waves, ring, max_k, max_strips, max_groups;
   size_t smem_bytes;
 } dw4_chain_plan;
 
