@@ -102,6 +102,19 @@ struct Share {
   uint32_t kcmag;
 };
 
+// A link as the streaming waves see it, written once per launch into LDS by
+// the control wave (the link table itself is read through the scalar cache,
+// whose misses cost the streaming waves hundreds of cycles at every link).
+struct LinkRec {
+  const unsigned char* pq;  // packed words of the link
+  int lin0;                 // first chunk (strip * KC) of this workgroup's share
+  int units;                // chunks in the share (ns * KC)
+  int kc_ns;                // KC | ns << 16
+  int G;
+  uint32_t gmag, kcmag;
+};
+static_assert(sizeof(LinkRec) == 32, "LDS link record");
+
 __device__ __forceinline__ Share share_of(const ChainLinkDev& L, int wg, int W, uint32_t wmag) {
   Share s;
   s.KC = L.K / kChunkK;
@@ -142,7 +155,30 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
   const size_t xbytes = ((size_t)M * max_k * 2 + 15) & ~(size_t)15;
   f4* part = reinterpret_cast<f4*>(smem + xbytes);
   unsigned char* meta = smem + xbytes + (size_t)2 * SW * max_strips * 256;
-  unsigned char* rings = meta + (size_t)2 * (meta_s + meta_z);
+  LinkRec* recs = reinterpret_cast<LinkRec*>(meta + (size_t)2 * (meta_s + meta_z));
+  unsigned char* rings = reinterpret_cast<unsigned char*>(recs + count);
+
+  if (wave == 0) {  // the streaming waves' link records, one lane per link
+    for (int li = lane; li < count; li += 64) {
+      const ChainLinkDev* L = links + li;
+      const int K = L->K, N = L->N, rot = L->rot;
+      const int KC = K / kChunkK, S = N / kStripN;
+      int r = wg + rot;
+      if (r >= W) r -= W;
+      const int sb = W == 1 ? 0 : (int)__umulhi((uint32_t)(r * S), wmag);
+      const int se = W == 1 ? S : (int)__umulhi((uint32_t)((r + 1) * S), wmag);
+      LinkRec rec;
+      rec.pq = reinterpret_cast<const unsigned char*>(L->pq);
+      rec.lin0 = sb * KC;
+      rec.units = (se - sb) * KC;
+      rec.kc_ns = KC | ((se - sb) << 16);
+      rec.G = L->G;
+      rec.gmag = L->gmag;
+      rec.kcmag = L->kcmag;
+      recs[li] = rec;
+    }
+  }
+  bare_barrier();  // link records in LDS
 
   if (wave == 0) {
     // ------------------------------------------------------------ control
@@ -304,11 +340,14 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
   int plin = 0, pend = 0;  // the next unit to copy, the end of the share
   const unsigned char* pqb = nullptr;
   auto p_enter = [&](int over) {  // link pl, `over` units into its share
-    const ChainLinkDev& L = links[pl];
-    const Share sh = share_of(L, wg, W, wmag);
-    plin = __builtin_amdgcn_readfirstlane(sh.sb * sh.KC + over);
-    pend = __builtin_amdgcn_readfirstlane((sh.sb + sh.ns) * sh.KC);
-    pqb = reinterpret_cast<const unsigned char*>(L.pq);
+    const LinkRec& r = recs[pl];
+    const int lin0 = __builtin_amdgcn_readfirstlane(r.lin0);
+    plin = lin0 + over;
+    pend = lin0 + __builtin_amdgcn_readfirstlane(r.units);
+    const uint64_t q = reinterpret_cast<uint64_t>(r.pq);
+    pqb = reinterpret_cast<const unsigned char*>(
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(q >> 32)) << 32) |
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)q));
   };
   auto p_settle = [&]() {  // move past shares the cursor has run off
     while (pl < count && plin >= pend) {
@@ -318,11 +357,12 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
     }
   };
   p_enter(ws);
+  const unsigned char* lq0 = pqb;  // link 0's packed words
   p_settle();
   // Past the end of the chain a wave re-copies a valid unit (its last real
   // one, or link 0's first chunk if it had none) into slots nothing reads
   // again, so the count of outstanding copies never changes.
-  const unsigned char* lq = reinterpret_cast<const unsigned char*>(links[0].pq);
+  const unsigned char* lq = lq0;
   const uint32_t voff16 = lane * 16;
   auto issue = [&](int slot) {
     if (pl < count) {
@@ -349,8 +389,13 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
   };
   for (int li = 0; li < count; ++li) {
     bare_barrier();  // activations and records of link li in LDS
-    const ChainLinkDev& L = links[li];
-    const Share sh = share_of(L, wg, W, wmag);
+    const LinkRec& rec = recs[li];
+    const int kc_ns = __builtin_amdgcn_readfirstlane(rec.kc_ns);
+    Share sh;
+    sh.KC = kc_ns & 0xffff;
+    sh.ns = kc_ns >> 16;
+    sh.units = __builtin_amdgcn_readfirstlane(rec.units);
+    sh.kcmag = (uint32_t)__builtin_amdgcn_readfirstlane((int)rec.kcmag);
     f4* pp = part + ((size_t)(li & 1) * SW + ws) * max_strips * 16;
     if (lane < 16)
       for (int sl = 0; sl < sh.ns; ++sl) pp[sl * 16 + lane] = f4{0.f, 0.f, 0.f, 0.f};
@@ -358,12 +403,12 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
       // A rows: lanes past the last row read row M - 1 (those MFMA output
       // rows are never stored)
       const unsigned char* xrow = reinterpret_cast<const unsigned char*>(xbuf) +
-                                  (size_t)(min(j, M - 1) * L.K + kq * 8) * 2;
+                                  (size_t)(min(j, M - 1) * sh.KC * kChunkK + kq * 8) * 2;
       const unsigned char* area = meta + (size_t)(li & 1) * (meta_s + meta_z);
       const unsigned char* srec = area + (j >> 1) * 4;           // + record * 32
       const unsigned char* zrec = area + meta_s + (j >> 3) * 4;  // + record * 8
-      const int G = L.G;
-      const uint32_t gmag = L.gmag;
+      const int G = __builtin_amdgcn_readfirstlane(rec.G);
+      const uint32_t gmag = (uint32_t)__builtin_amdgcn_readfirstlane((int)rec.gmag);
       int sl = sh.kcmag == 0 ? cu : (int)__umulhi((uint32_t)cu, sh.kcmag);
       int c = cu - sl * sh.KC;
       int cur = sl;
@@ -444,17 +489,19 @@ size_t chain_meta_bytes(int max_strips, int max_groups, bool zeros) {
                : (((size_t)max_strips * max_groups * 32 + 1023) & ~(size_t)1023);
 }
 
-size_t chain_smem_bytes(int m, int max_k, int max_strips, int max_groups, int waves, int ring) {
+size_t chain_smem_bytes(int m, int max_k, int max_strips, int max_groups, int count, int waves,
+                        int ring) {
   return (((size_t)m * max_k * 2 + 15) & ~(size_t)15) + (size_t)2 * waves * max_strips * 256 +
          2 * (chain_meta_bytes(max_strips, max_groups, false) +
               chain_meta_bytes(max_strips, max_groups, true)) +
-         (size_t)waves * ring * kSlot;
+         (size_t)count * sizeof(LinkRec) + (size_t)waves * ring * kSlot;
 }
 
 bool plan_chain(ChainPlan& p) {
   p.waves = kChainWaves;
   for (int r : kRings) {
-    const size_t b = chain_smem_bytes(p.m, p.max_k, p.max_strips, p.max_groups, p.waves, r);
+    const size_t b =
+        chain_smem_bytes(p.m, p.max_k, p.max_strips, p.max_groups, p.count, p.waves, r);
     if (b <= kLdsPerCu) {
       p.ring = r;
       p.smem = b;

@@ -446,7 +446,8 @@ struct ChainPlan {
   size_t smem;
 };
 // LDS bytes of a chain workgroup for a plan's ring depth.
-size_t chain_smem_bytes(int m, int max_k, int max_strips, int max_groups, int waves, int ring);
+size_t chain_smem_bytes(int m, int max_k, int max_strips, int max_groups, int count, int waves,
+                        int ring);
 // Picks the ring depth (units in flight per streaming wave) and LDS size.
 bool plan_chain(ChainPlan& p);
 hipError_t launch_chain(const ChainPlan& p, void* chain, hipStream_t stream);
