@@ -1,6 +1,6 @@
 // C ABI of libdrofell_w4a16.so (declared in include/drofell_w4a16.h).
 //
-// Validation and dispatch live here; the kernels are in w4a16_kernels.hip.
+// Validation and dispatch live here; the kernels are in the other w4a16_*.hip files.
 // Every entry point returns a status code; nothing throws across the ABI.
 
 #include <hip/hip_runtime.h>
@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "drofell_w4a16.h"
+#include "w4a16_chain.h"
 #include "w4a16_internal.h"
 
 namespace {

@@ -44,7 +44,7 @@
 #include <stdint.h>
 
 #include "w4a16_device.h"
-#include "w4a16_internal.h"
+#include "w4a16_chain.h"
 
 namespace dw4 {
 
