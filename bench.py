@@ -6,14 +6,19 @@ gate, up, down) of 8 Llama-2-7B layers -- one pipeline stage of the
 reference's split model (8 of the 32 decoder layers) with the
 GPTQ 4-bit quantisation (group 128, asymmetric zeros).  The 56 packed weight
 matrices (842 MB) are distinct, four times the 256 MB Infinity Cache, so
-every launch streams its weights from HBM.  The step is captured once into
-a HIP graph and replayed; timing uses HIP events on the replay stream.
+every launch streams its weights from HBM.  The projections run in a
+decoder layer's data-flow order with the fewest launches it allows: q, k, v
+(same input) in one grouped launch, o, gate and up (same input) in one
+grouped launch, down -- 32 launches per step; the 56-launch form (one per
+projection) is reported beside it.  The step is captured once into a HIP
+graph and replayed; timing uses HIP events on the replay stream.
 
 Printed JSON line: ``value`` = algorithmic bytes moved per second (GB/s) at
 M=1, ``roofline`` for the decode kernel (the only kernel in the step),
 ``prefill`` = the same 56 GEMMs at M=256 in TFLOP/s against the fp16 MFMA
 peak, ``cpu_baseline`` = the reference's CPU dequantise-then-matmul path
-(restated with torch CPU ops) on a bounded sample.
+(restated with torch CPU ops) on a bounded sample, timed in its dequantise,
+matmul and combined phases.
 """
 from __future__ import annotations
 
@@ -122,7 +127,7 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None, per_repl
     return ms, wall, sel
 
 
-DECODE_SOURCES = ("w4a16_kernels.hip", "w4a16_internal.h", "w4a16_device.h")
+DECODE_SOURCES = ("w4a16_decode.hip", "w4a16_internal.h", "w4a16_device.h")
 
 
 def decode_source_sha256() -> str:
@@ -221,8 +226,6 @@ def device_peaks(dev, steps: int) -> dict:
     roofline fractions (which stay against the spec peaks): a large fp16
     library GEMM (torch.matmul, hipBLASLt), a 1 GiB device copy and the
     library's streaming read over 1 GiB, each captured in a HIP graph."""
-    import subprocess
-
     import torch
     from hip_extends import _lib
 
@@ -252,11 +255,8 @@ def device_peaks(dev, steps: int) -> dict:
     rec["stream_read_1GiB"] = {"ms": round(ms, 4), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     del src, sink
     torch.cuda.empty_cache()
-    try:  # current clocks, as the SMI reports them (informational)
-        smi = subprocess.run(["rocm-smi", "--showclocks"], capture_output=True, text=True, timeout=20)
-        rec["clocks"] = [ln.strip() for ln in smi.stdout.splitlines() if "Mhz" in ln or "MHz" in ln][:8]
-    except (OSError, subprocess.SubprocessError):
-        rec["clocks"] = None
+    info = device_info(dev)  # current clock levels after the runs (informational)
+    rec["clocks"] = {"sclk": info["sclk"], "mclk": info["mclk"]}
     log(json.dumps({"device_peaks": rec}))
     return rec
 
@@ -538,7 +538,10 @@ def host_cpu() -> dict:
 
 
 def cpu_baseline(seconds: float) -> dict:
-    """The reference's CPU dequantise-then-matmul on one 4096x4096 projection."""
+    """The reference's CPU dequantise-then-matmul on one 4096x4096 projection,
+    timed in its three phases: dequantise (reconstruct the fp16 weight), the
+    fp32 matmul against an already dequantised weight, and both back to back
+    (the reference's forward).  ``value`` is the combined phase's rate."""
     import statistics
 
     import torch
@@ -550,20 +553,176 @@ def cpu_baseline(seconds: float) -> dict:
     torch.set_num_threads(threads)
     lay = make_layer(4096, 4096, GROUP, seed=1000)
     x = make_x(1, 4096, seed=1)
-    cpu_path.forward(x, lay.qweight, lay.qzeros, lay.scales, lay.g_idx)  # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or time.perf_counter() < t_end:
-        t0 = time.perf_counter_ns()
-        cpu_path.forward(x, lay.qweight, lay.qzeros, lay.scales, lay.g_idx)
-        times.append((time.perf_counter_ns() - t0) * 1e-9)
-    med = statistics.median(times)
+    w = cpu_path.reconstruct_weights(lay.qweight, lay.qzeros, lay.scales, lay.g_idx)
+    phases = {
+        "dequantise": lambda: cpu_path.reconstruct_weights(lay.qweight, lay.qzeros, lay.scales,
+                                                           lay.g_idx),
+        "matmul": lambda: (x.float() @ w.float()).to(torch.float16),
+        "both": lambda: cpu_path.forward(x, lay.qweight, lay.qzeros, lay.scales, lay.g_idx),
+    }
+    share = {"dequantise": 0.3, "matmul": 0.2, "both": 0.5}
+    med, runs = {}, {}
+    for name, fn in phases.items():
+        fn()  # warm-up
+        times = []
+        t_end = time.perf_counter() + seconds * share[name]
+        while len(times) < 3 or time.perf_counter() < t_end:
+            t0 = time.perf_counter_ns()
+            fn()
+            times.append((time.perf_counter_ns() - t0) * 1e-9)
+        med[name], runs[name] = statistics.median(times), len(times)
     nbytes = algorithmic_bytes(1, 4096, 4096, GROUP, False)
-    return {"value": round(nbytes / med / 1e9, 4), "unit": "GB/s", "cores": threads,
+    return {"value": round(nbytes / med["both"] / 1e9, 4), "unit": "GB/s", "cores": threads,
             **host_cpu(), "kind": "port",
+            "phases_ms": {k: round(v * 1e3, 3) for k, v in med.items()},
             "sample": (f"torch-CPU dequantise+matmul (real_quant.py:69-102 restated) of one "
-                       f"4096x4096 g128 asymmetric projection at M=1, {len(times)} runs, "
-                       f"median {med * 1e3:.1f} ms; torch {torch.__version__}")}
+                       f"4096x4096 g128 asymmetric projection at M=1; median of "
+                       f"{runs['dequantise']} / {runs['matmul']} / {runs['both']} runs of the "
+                       f"dequantise / matmul / combined phases; torch {torch.__version__}")}
+
+
+def device_info(dev) -> dict:
+    """GPU name, architecture, CU count, ROCm/HIP version and the current
+    shader and memory clock levels (None where a field is not available).
+    The clocks and the product name come from the amdgpu sysfs files of the
+    card whose PCI address matches the device (no child process: this runs
+    after the GPU is initialised)."""
+    import glob
+
+    import torch
+    props = torch.cuda.get_device_properties(dev)
+    info = {"gpu": props.name, "arch": getattr(props, "gcnArchName", None),
+            "cus": props.multi_processor_count, "hip": torch.version.hip,
+            "torch": torch.__version__, "rocm": None, "product": None, "pci": None,
+            "sclk": None, "mclk": None}
+    try:
+        with open("/opt/rocm/.info/version") as f:
+            info["rocm"] = f.read().strip()
+    except OSError:
+        pass
+    bus = getattr(props, "pci_bus_id", None)
+    dom = getattr(props, "pci_domain_id", 0) or 0
+    devn = getattr(props, "pci_device_id", 0) or 0
+    if bus is None:
+        return info
+    info["pci"] = f"{dom:04x}:{bus:02x}:{devn:02x}.0"
+
+    def read(path):
+        try:
+            with open(path) as f:
+                return f.read()
+        except OSError:
+            return None
+
+    for card in glob.glob("/sys/class/drm/card*/device"):
+        if not os.path.realpath(card).endswith(info["pci"]):
+            continue
+        name = read(os.path.join(card, "product_name"))
+        info["product"] = name.strip() if name else None
+        for key, fname in (("sclk", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
+            levels = read(os.path.join(card, fname)) or ""
+            cur = [ln.split(":", 1)[-1].replace("*", "").strip()
+                   for ln in levels.splitlines() if ln.rstrip().endswith("*")]
+            info[key] = cur[0] if cur else None
+        break
+    return info
+
+
+def grouped_leg(mats, dev, steps: int, warmup: int) -> dict:
+    """The 56 projections of the decode leg with the launches a decoder
+    layer's data flow allows: q, k, v share the layer input (one
+    dw4_gemm_group launch), o alone, gate and up share o's output (one
+    launch), down alone -- 4 launches per layer instead of 7.  Same
+    matrices, same bytes."""
+    import torch
+    from gptq_synth import algorithmic_bytes
+    from hip_extends.w4a16 import gemm_group
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+    xs = {k: torch.randn(1, k, device=dev, generator=gen).to(torch.float16)
+          for k in sorted({t[1] for t in mats})}
+    groups = []
+    for li in range(len(mats) // 7):
+        w = {name.split("_")[0]: (q4, k, n) for name, k, n, q4 in mats[7 * li:7 * li + 7]}
+        for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            k = w[names[0]][1]
+            outs = [torch.empty(1, w[nm][2], dtype=torch.float16, device=dev) for nm in names]
+            groups.append((xs[k], [w[nm][0] for nm in names], outs))
+
+    def one_pass():
+        for x, q4s, outs in groups:
+            if len(q4s) == 1:
+                q4s[0].matmul(x, output=outs[0])
+            else:
+                gemm_group(x, q4s, outs)
+
+    ms = time_callable(one_pass, steps, warmup, dev)
+    nbytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"decode M=1: {ms * 1e3:.1f} us per step ({len(groups)} launches), {gbs:.1f} GB/s")
+    return {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "launches_per_step": len(groups),
+            "kernel": "dw4::decode_kernel (item table over q/k/v and gate/up)"}
+
+
+def chain_leg(mats, dev, steps: int, warmup: int, layers: int) -> dict:
+    """The 56 projections of the decode leg as ONE dw4_gemm_chain launch per
+    step, in two forms:
+
+    * ``dependent``: each layer's data flow (q, k, v read the layer input; o
+      reads v's output with the layer input as residual; gate and up read
+      o's output; down reads up's output with o's output as residual and
+      writes the next layer's input), so every link waits for the link it
+      reads to complete on all workgroups;
+    * ``independent``: every link reads a fixed activation (no waits), the
+      same work as the per-launch decode leg.
+
+    Both move the same algorithmic bytes as the decode leg."""
+    import torch
+    from gptq_synth import algorithmic_bytes
+    from hip_extends.chain import ChainStep, Q4Chain
+
+    f16 = dict(dtype=torch.float16, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    nbytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
+    xs = {k: torch.randn(1, k, device=dev, generator=gen).to(torch.float16)
+          for k in sorted({t[1] for t in mats})}
+    ind = [ChainStep(q4, xs[k], torch.empty(1, n, **f16)) for _, k, n, q4 in mats]
+    hidden = mats[0][1]
+    hs = [torch.randn(1, hidden, device=dev, generator=gen).to(torch.float16)
+          for _ in range(layers + 1)]
+    dep, down = [], -1
+    for li in range(layers):
+        w = {name.split("_")[0]: (q4, n) for name, _, n, q4 in mats[7 * li:7 * li + 7]}
+        out = {name: torch.empty(1, n, **f16) for name, (_, n) in w.items()}
+        base = len(dep)
+        dep += [ChainStep(w["q"][0], hs[li], out["q"], down),
+                ChainStep(w["k"][0], hs[li], out["k"], down),
+                ChainStep(w["v"][0], hs[li], out["v"], down),
+                ChainStep(w["o"][0], out["v"], out["o"], base + 2, residual=hs[li]),
+                ChainStep(w["gate"][0], out["o"], out["gate"], base + 3),
+                ChainStep(w["up"][0], out["o"], out["up"], base + 3),
+                ChainStep(w["down"][0], out["up"], hs[li + 1], base + 5, residual=out["o"])]
+        down = base + 6
+    res = {"kernel": "dw4::chain_kernel", "links": len(mats), "launches_per_step": 1,
+           "algorithmic_bytes_per_step": nbytes}
+    for name, links in (("dependent", dep), ("independent", ind)):
+        chain = Q4Chain(links, 1)
+        chain.run()
+        torch.cuda.synchronize(dev)
+        ms = time_callable(chain.run, steps, warmup, dev)
+        if chain.timed_out():
+            raise RuntimeError(f"chain leg ({name}): a dependency wait gave up")
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"chain ({name}) M=1: {ms * 1e3:.1f} us per step, {gbs:.1f} GB/s "
+            f"(ring {chain.plan.ring}, {chain.plan.workgroups} workgroups)")
+        res[name] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "ring": chain.plan.ring,
+                     "workgroups": chain.plan.workgroups, "waves": chain.plan.waves}
+        del chain
+    return res
 
 
 def time_transpose(mats, m: int, steps: int, warmup: int, dev, dense: bool = False) -> float:
@@ -706,6 +865,11 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="per-shape/per-M table on stderr")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config points (configs 1-4) of the JSON line")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline decode step and print its line (for counter "
+                         "passes)")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the one-launch decode chain leg")
     ap.add_argument("--no-transpose", action="store_true",
                     help="skip the transposed (PEFT backward) leg")
     ap.add_argument("--no-stage", action="store_true",
@@ -766,11 +930,11 @@ def main() -> int:
         tf = sum(flops(m, k, n) for _, k, n, _ in mats) / (pms * 1e-3) / 1e12
         log(f"prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
         return 0
-    ms, wall, _ = time_graph(mats, 1, args.steps, args.warmup, dev)
     step_bytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
+    grouped = grouped_leg(mats, dev, args.steps, args.warmup)
+    ms = grouped["us_per_step"] * 1e-3
+    launches = grouped["launches_per_step"]
     gbs = step_bytes / (ms * 1e-3) / 1e9
-    log(f"decode M=1: {ms * 1e3:.1f} us per step ({len(mats)} GEMMs), {gbs:.1f} GB/s, "
-        f"wall {wall:.3f} s")
 
     result = {
         "metric": METRIC,
@@ -788,14 +952,19 @@ def main() -> int:
         "config": {
             "workload": ("llama2-7b 8-layer stage decode, 7 GPTQ projections per layer "
                          "(4x 4096x4096, 2x 4096x11008, 1x 11008x4096), M=1, group 128, "
-                         "asymmetric zeros; 56 distinct weight matrices per step"),
+                         "asymmetric zeros; 56 distinct weight matrices per step, each with its "
+                         "own output, launched in the layer's data-flow order: q/k/v in one "
+                         "grouped launch (they share the layer input), o, gate/up in one grouped "
+                         "launch (they share o's output), down"),
             "m": 1, "layers": args.layers, "group_size": GROUP,
             "weight_bytes": weight_bytes, "algorithmic_bytes_per_step": step_bytes,
-            "launches_per_step": len(mats), "hip_graph": True,
+            "matrices_per_step": len(mats), "launches_per_step": launches, "hip_graph": True,
         },
-        # Dominant (only) kernel of the step: dw4::decode_kernel.  Algorithmic
-        # bytes per launch (mean over the 56 launches) / mean launch duration
-        # (HIP events around the graph replays on the replay stream / 56).
+        "device": device_info(dev),
+        # Dominant (only) kernel of the step: dw4::decode_kernel (single-matrix
+        # and item-table forms).  Algorithmic bytes per launch (mean over the
+        # step's launches) / mean launch duration (HIP events around the graph
+        # replays on the replay stream / launches).
         "roofline": {
             "bound": "hbm",
             "achieved": round(gbs, 2),
@@ -804,23 +973,39 @@ def main() -> int:
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
             "kernel": "dw4::decode_kernel",
-            "bytes_per_launch": step_bytes // len(mats),
-            "avg_launch_us": round(ms * 1e3 / len(mats), 3),
+            "bytes_per_launch": step_bytes // launches,
+            "avg_launch_us": round(ms * 1e3 / launches, 3),
         },
     }
 
-    # Measured HBM bytes per launch (two calibrated rocprofv3 counter passes),
-    # used only while the decode kernel's sources are the ones it was
-    # measured on.
+    # Measured HBM bytes per launch (two calibrated rocprofv3 counter passes
+    # over this step), used only while the decode kernel's sources are the
+    # ones it was measured on.
     traffic_file = os.path.join(REPO, "profiles", "decode_traffic.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as f:
             rec = json.load(f)
-        if rec.get("source_sha256") == decode_source_sha256():
+        if rec.get("source_sha256") == decode_source_sha256() and \
+                rec.get("launches_per_step") == launches:
             result["roofline"]["traffic"] = rec.get("hbm_bytes_per_launch")
         else:
             result["roofline"]["traffic_note"] = ("profiles/decode_traffic.json was measured on "
-                                                  "other decode kernel sources")
+                                                  "other decode kernel sources or another step")
+    if args.headline_only:
+        print(json.dumps(result), flush=True)
+        return 0
+
+    # the same step with one launch per projection (56 launches)
+    pms, wall, _ = time_graph(mats, 1, args.steps, args.warmup, dev)
+    pg = step_bytes / (pms * 1e-3) / 1e9
+    log(f"decode M=1, one launch per projection: {pms * 1e3:.1f} us per step ({len(mats)} "
+        f"launches), {pg:.1f} GB/s, wall {wall:.3f} s")
+    result["per_projection_launches"] = {"us_per_step": round(pms * 1e3, 2), "GB/s": round(pg, 1),
+                                         "frac": round(pg / HBM_PEAK_GBS, 4),
+                                         "launches_per_step": len(mats)}
+
+    if not args.no_chain:
+        result["chain"] = chain_leg(mats, dev, args.steps, args.warmup, args.layers)
 
     if not args.no_prefill:
         m = args.prefill_m
