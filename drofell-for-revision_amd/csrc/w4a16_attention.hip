@@ -34,8 +34,6 @@ namespace dw4 {
 
 namespace {
 
-constexpr int kAttnThreads = 256;
-constexpr int kAttnWaves = kAttnThreads / 64;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -49,8 +47,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Block-wide reduction in a fixed order (waves' results summed 0..3).
-template <bool MAX>
+// Block-wide reduction in a fixed order (waves' results combined 0..W-1).
+template <bool MAX, int W>
 __device__ __forceinline__ float block_reduce(float v, float* scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v = MAX ? wave_max(v) : wave_sum(v);
@@ -59,12 +57,15 @@ __device__ __forceinline__ float block_reduce(float v, float* scratch) {
   __syncthreads();
   float r = scratch[0];
 #pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
+  for (int w = 1; w < W; ++w) r = MAX ? fmaxf(r, scratch[w]) : r + scratch[w];
   return r;
 }
 
-template <int HS, int BS, int GMAX>
-__global__ void __launch_bounds__(kAttnThreads)
+// W waves per workgroup: 4 (several partitions per (sequence, kv head),
+// about four workgroups per CU) or 16 (one workgroup per (sequence, kv head)
+// covering the whole context, no combine launch).
+template <int HS, int BS, int GMAX, int W>
+__global__ void __launch_bounds__(W * 64)
 paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
                        uint16_t* __restrict__ out, int64_t o_stride,
                        const int64_t* __restrict__ kptr, const int64_t* __restrict__ vptr,
@@ -86,7 +87,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   float* qs = sm;                           // [G][HS] fp32 query (scaled)
   float* logit = qs + GMAX * HS;            // [G][part_tokens]
   float* red = logit + GMAX * part_tokens;  // [waves][G][HS] partial outputs
-  float* scratch = red + kAttnWaves * GMAX * HS;  // 8 floats
+  float* scratch = red + W * GMAX * HS;  // W floats
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -108,7 +109,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
     }
     return;
   }
-  for (int i = tid; i < G * HS; i += kAttnThreads) {
+  for (int i = tid; i < G * HS; i += (W * 64)) {
     const int g = i / HS, d = i % HS;
     qs[i] = scale * (float)as_h(query[(size_t)seq * q_stride + (size_t)(h0 + g) * HS + d]);
   }
@@ -116,7 +117,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
 
   const int32_t* btab = block_tables + (size_t)seq * max_blocks + t0 / BS;
   const int nb = (nt + BS - 1) / BS;
-  const int nbw = wave < nb ? (nb - wave + kAttnWaves - 1) / kAttnWaves : 0;  // this wave's blocks
+  const int nbw = wave < nb ? (nb - wave + W - 1) / W : 0;  // this wave's blocks
   const int tt = lane % BS;   // token of this lane within a block
   const int sg = lane / BS;   // slice group
   // Each wave keeps its next NPF blocks' keys and values in flight: the
@@ -127,11 +128,11 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
   h8 kreg[NPF][SPL];
   h8 vreg[NPF][DPL][BS / 8];
   auto kbase = [&](int i) {
-    return reinterpret_cast<const uint16_t*>(kptr[btab[wave + kAttnWaves * i]]) +
+    return reinterpret_cast<const uint16_t*>(kptr[btab[wave + W * i]]) +
            (size_t)kvh * kv_head_stride;
   };
   auto vbase = [&](int i) {
-    return reinterpret_cast<const uint16_t*>(vptr[btab[wave + kAttnWaves * i]]) +
+    return reinterpret_cast<const uint16_t*>(vptr[btab[wave + W * i]]) +
            (size_t)kvh * kv_head_stride;
   };
   auto load_k = [&](int slot, int i) {
@@ -164,7 +165,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
 
   // q . k
   auto qk = [&](int slot, int i) {
-    const int b = wave + kAttnWaves * i;
+    const int b = wave + W * i;
     float dot[GMAX];
 #pragma unroll
     for (int g = 0; g < GMAX; ++g) {
@@ -216,15 +217,15 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
     sum[g] = 0.f;
     if (g < G) {
       float m = -FLT_MAX;
-      for (int t = tid; t < nt; t += kAttnThreads) m = fmaxf(m, logit[g * part_tokens + t]);
-      mx[g] = block_reduce<true>(m, scratch);
+      for (int t = tid; t < nt; t += (W * 64)) m = fmaxf(m, logit[g * part_tokens + t]);
+      mx[g] = block_reduce<true, W>(m, scratch);
       float s = 0.f;
-      for (int t = tid; t < nb * BS; t += kAttnThreads) {
+      for (int t = tid; t < nb * BS; t += (W * 64)) {
         const float p = t < nt ? __expf(logit[g * part_tokens + t] - mx[g]) : 0.f;
         logit[g * part_tokens + t] = p;
         s += p;
       }
-      sum[g] = block_reduce<false>(s, scratch);
+      sum[g] = block_reduce<false, W>(s, scratch);
     }
   }
   __syncthreads();
@@ -236,7 +237,7 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
   auto pv = [&](int slot, int i) {
-    const int b = wave + kAttnWaves * i;
+    const int b = wave + W * i;
     const int valid = min(BS, nt - b * BS);  // tokens of this block in the context
 #pragma unroll
     for (int j = 0; j < DPL; ++j)
@@ -268,11 +269,11 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
     for (int j = 0; j < DPL; ++j)
       if (g < G && (!VTAIL || lane + 64 * j < HS)) red[(wave * GMAX + g) * HS + lane + 64 * j] = acc[g][j];
   __syncthreads();
-  for (int i = tid; i < G * HS; i += kAttnThreads) {
+  for (int i = tid; i < G * HS; i += (W * 64)) {
     const int g = i / HS, d = i % HS;
     float o = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) o += red[(w * GMAX + g) * HS + d];
+    for (int w = 0; w < W; ++w) o += red[(w * GMAX + g) * HS + d];
     float s = 0.f, m = 0.f;
 #pragma unroll
     for (int gg = 0; gg < GMAX; ++gg)
@@ -360,20 +361,34 @@ __global__ void reshape_and_cache_kernel(uint16_t* __restrict__ key, int64_t key
   }
 }
 
-template <int HS, int BS, int GMAX>
-hipError_t launch_pa(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
-                     hipStream_t stream) {
-  const size_t smem = sizeof(float) * ((size_t)GMAX * HS + (size_t)GMAX * p.part_tokens +
-                                       (size_t)kAttnWaves * GMAX * HS + 8);
+template <int HS, int BS, int GMAX, int W>
+hipError_t launch_pa_w(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                       hipStream_t stream) {
+  const size_t smem = attn_smem_bytes(HS, GMAX, p.part_tokens, W);
   const dim3 grid((unsigned)(a.num_seqs * a.num_kv_heads), (unsigned)p.num_parts);
   float* ws_ml = p.num_parts > 1 ? ws : nullptr;
   float* ws_out = p.num_parts > 1 ? ws + 2 * (size_t)a.num_seqs * a.num_heads * p.num_parts : nullptr;
-  paged_attention_kernel<HS, BS, GMAX><<<grid, kAttnThreads, smem, stream>>>(
+  paged_attention_kernel<HS, BS, GMAX, W><<<grid, W * 64, smem, stream>>>(
       a.query, a.q_stride, a.out, a.o_stride, a.kptr, a.vptr, a.kv_head_stride, a.num_heads,
       a.num_kv_heads, a.scale, a.block_tables, a.max_blocks, a.context_lens, a.alibi,
       p.part_tokens, p.num_parts, ws_ml, ws_out);
-  hipError_t e = hipGetLastError();
+  return hipGetLastError();
+}
+
+template <int HS, int BS, int GMAX>
+hipError_t launch_pa(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,
+                     hipStream_t stream) {
+  hipError_t e;
+  if constexpr (attn_wide_ok(HS, BS, GMAX)) {
+    e = p.waves == 16 ? launch_pa_w<HS, BS, GMAX, 16>(a, p, ws, stream)
+                      : launch_pa_w<HS, BS, GMAX, 4>(a, p, ws, stream);
+  } else {
+    if (p.waves != 4) return hipErrorInvalidValue;
+    e = launch_pa_w<HS, BS, GMAX, 4>(a, p, ws, stream);
+  }
   if (e != hipSuccess || p.num_parts == 1) return e;
+  float* ws_ml = ws;
+  float* ws_out = ws + 2 * (size_t)a.num_seqs * a.num_heads * p.num_parts;
   paged_attention_reduce_kernel<HS><<<(unsigned)(a.num_seqs * a.num_heads), HS, 0, stream>>>(
       a.out, a.o_stride, a.num_heads, a.context_lens, a.max_blocks * BS, p.part_tokens,
       p.num_parts, ws_ml, ws_out);
@@ -504,13 +519,26 @@ hipError_t launch_rope(uint16_t* x, const uint16_t* sinp, const uint16_t* cosp, 
   return hipGetLastError();
 }
 
-PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_size,
-                                   int max_context_len, int cus) {
+PagedAttnPlan plan_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_size,
+                                   int block_size, int max_context_len, int cus) {
   PagedAttnPlan p;
   const int blocks = std::max(1, (max_context_len + block_size - 1) / block_size);
+  const int pairs = std::max(1, num_seqs * num_kv_heads);
+  // one 16-wave workgroup per (sequence, kv head) over the whole context
+  // where that gives every CU about one workgroup and the context fits one
+  // partition: no combine launch
+  const int g = num_kv_heads > 0 ? num_heads / num_kv_heads : 1;
+  const int gmax = g == 1 ? 1 : g <= 4 ? 4 : 8;
+  if (attn_wide_ok(head_size, block_size, gmax) && 2 * pairs > cus && pairs <= cus &&
+      blocks * block_size <= kAttnWideMaxTokens &&
+      attn_smem_bytes(head_size, gmax, blocks * block_size, 16) <= 64 * 1024) {
+    p.waves = 16;
+    p.part_tokens = blocks * block_size;
+    p.num_parts = 1;
+    return p;
+  }
   // about four workgroups per CU (eight measured no faster); partitions of
   // whole blocks, at most 512 tokens
-  const int pairs = std::max(1, num_seqs * num_kv_heads);
   int parts = std::max(1, (4 * cus + pairs - 1) / pairs);
   parts = std::min(parts, blocks);
   int bpp = (blocks + parts - 1) / parts;

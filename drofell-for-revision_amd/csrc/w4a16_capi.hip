@@ -516,7 +516,7 @@ int dw4_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_h
                                   max_context_len);
   if (st != DW4_OK) return st;
   if (workspace_bytes == nullptr) return DW4_ERR_INVALID_ARG;
-  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_kv_heads, block_size,
+  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_heads, num_kv_heads, head_size, block_size,
                                                          max_context_len, cu_count());
   *workspace_bytes = num_seqs == 0 ? 0 : dw4::paged_attention_ws_bytes(p, num_seqs, num_heads, head_size);
   return DW4_OK;
@@ -541,7 +541,7 @@ int dw4_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_
       max_context_len < 1 || max_blocks_per_seq * block_size < max_context_len)
     return DW4_ERR_INVALID_ARG;
   if (!aligned16(query) || q_stride % 8 != 0) return DW4_ERR_MISALIGNED;
-  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_kv_heads, block_size,
+  const dw4::PagedAttnPlan p = dw4::plan_paged_attention(num_seqs, num_heads, num_kv_heads, head_size, block_size,
                                                          max_context_len, cu_count());
   const size_t need = dw4::paged_attention_ws_bytes(p, num_seqs, num_heads, head_size);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return DW4_ERR_WORKSPACE;

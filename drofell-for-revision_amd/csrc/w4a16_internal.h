@@ -349,9 +349,24 @@ struct PagedAttnArgs {
 struct PagedAttnPlan {
   int part_tokens = kAttnMaxPartTokens;
   int num_parts = 1;
+  int waves = 4;  // per workgroup: 4, or 16 for one workgroup per (sequence, kv head)
 };
-PagedAttnPlan plan_paged_attention(int num_seqs, int num_kv_heads, int block_size,
-                                   int max_context_len, int cus);
+// The 16-wave form: contexts up to this many tokens in one partition, for
+// the (head size, block size, query-head group) variants whose per-wave
+// partial outputs fit LDS and whose registers fit 1024-thread workgroups.
+constexpr int kAttnWideMaxTokens = 1024;
+constexpr bool attn_wide_ok(int hs, int bs, int gmax) {
+  return bs == 16 && hs <= 128 && gmax * hs <= 512;
+}
+// Dynamic LDS of a paged-attention workgroup: the scaled queries [gmax][hs],
+// the logits [gmax][part_tokens], the waves' partial outputs
+// [waves][gmax][hs] and one float per wave for block reductions.
+inline size_t attn_smem_bytes(int hs, int gmax, int part_tokens, int waves) {
+  return sizeof(float) * ((size_t)gmax * hs + (size_t)gmax * part_tokens +
+                          (size_t)waves * gmax * hs + waves);
+}
+PagedAttnPlan plan_paged_attention(int num_seqs, int num_heads, int num_kv_heads, int head_size,
+                                   int block_size, int max_context_len, int cus);
 size_t paged_attention_ws_bytes(const PagedAttnPlan& p, int num_seqs, int num_heads,
                                 int head_size);
 hipError_t launch_paged_attention(const PagedAttnArgs& a, const PagedAttnPlan& p, float* ws,

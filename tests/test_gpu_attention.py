@@ -114,6 +114,14 @@ CASES = [
     ([260, 17], 16, 2, 96, 32, False),
     ([3, 100, 1100], 8, 1, 112, 16, False),
     ([45, 64], 4, 4, 112, 32, True),
+    # more than half as many (sequence, kv head) pairs as CUs, contexts up to
+    # 1024 tokens, 16-token blocks: one 16-wave workgroup per pair over the
+    # whole context (no combine launch) on a 256-CU device
+    ([1000, 3, 517, 64, 250, 1, 33, 768], 24, 24, 80, 16, False),
+    ([200, 1024, 7, 45, 96, 300, 12, 640], 96, 24, 96, 16, True),
+    ([129, 1, 800, 300], 384, 48, 64, 16, False),
+    ([5, 900, 333, 64, 1, 2], 128, 32, 112, 16, False),
+    ([1, 17, 1024, 511, 512, 33, 300, 64, 100], 64, 16, 128, 16, False),
 ]
 
 
@@ -184,6 +192,16 @@ def test_attention_statuses(hip_device):
     for hs in (64, 80, 96, 112, 128, 256):
         assert lib.dw4_paged_attention_workspace_size(2, 8, 8, hs, 16, 100,
                                                       ctypes.byref(sz)) == _lib.DW4_OK
+    if torch.cuda.get_device_properties(hip_device).multi_processor_count == 256:
+        # the stage shape (8 x 32 (sequence, kv head) pairs, 512 tokens): one
+        # 16-wave workgroup per pair, no partitions, no workspace; a small
+        # batch keeps the partitioned form
+        assert lib.dw4_paged_attention_workspace_size(8, 32, 32, 128, 16, 512,
+                                                      ctypes.byref(sz)) == _lib.DW4_OK
+        assert sz.value == 0
+        assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 128, 16, 512,
+                                                      ctypes.byref(sz)) == _lib.DW4_OK
+        assert sz.value > 0
     assert lib.dw4_paged_attention_workspace_size(2, 36, 4, 128, 16, 100, ctypes.byref(sz)) == \
         _lib.DW4_ERR_UNSUPPORTED  # 9 query heads per kv head
     assert lib.dw4_paged_attention_workspace_size(2, 8, 8, 128, 8, 100, ctypes.byref(sz)) == \
