@@ -121,7 +121,7 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
                 const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
                 uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ res,
                 int64_t ldres, float* __restrict__ part, int K, int N, int gs, int G,
-                int chunks_per_split, int mtiles, int ntiles, int splits) {
+                int chunks_per_split, int mtiles, int ntiles, int splits, int group_m) {
   using T = Tile<MTW, CG, GPC, W>;
   constexpr int kWaves = W;
   constexpr int kBM = T::kBM;
@@ -135,14 +135,23 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   __shared__ __attribute__((aligned(256))) unsigned char ring[S * T::kBytes];
 
   // XCD-aware order over units (column tile, K split), u = split * ntiles +
-  // ntile: workgroup b runs on XCD b % 8, and the row tiles of unit u are
-  // the workgroups congruent to u mod 8, so they share that XCD's L2 for the
-  // unit's weights, and every XCD gets ceil(units / 8) units
+  // ntile: workgroup b runs on XCD b % 8 and takes the XCD's (b / 8)-th
+  // (row tile, unit) pair; XCD x owns the units congruent to x mod 8
+  // (ceil(units / 8) each, the padding ones exit).  On one XCD the pairs
+  // run in groups of group_m row tiles: within a group, the row tiles of
+  // one unit are consecutive, then the next unit's, so the workgroups an
+  // XCD runs at once share both the units' weights and the group's
+  // activation rows in its L2 (group_m = all row tiles: every row tile of
+  // a unit on one XCD in turn).
   const int b = blockIdx.x;
-  const int q8 = b / (8 * mtiles);
-  const int r8 = b % (8 * mtiles);
-  const int mtile = r8 / 8;
-  const int unit = q8 * 8 + (r8 % 8);
+  const int nul = (ntiles * splits + 7) / 8;
+  const int pos = b >> 3;  // position in this XCD's order
+  const int grp = pos / (group_m * nul);
+  const int first_m = grp * group_m;
+  const int gsz = min(mtiles - first_m, group_m);
+  const int jj = pos - grp * group_m * nul;
+  const int mtile = first_m + jj % gsz;
+  const int unit = (jj / gsz) * 8 + (b & 7);
   if (unit >= ntiles * splits) return;
   const int ntile = unit % ntiles;
   const int split = unit / ntiles;
@@ -447,6 +456,14 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   }
 }
 
+// Row tiles per group of the workgroup order (kernel comment above): all of
+// them up to 8 (a unit's weights then come into an XCD's L2 once), groups of
+// 8 above.  Measured against one group at M=4096 (32 row tiles of 128):
+// 4096^2 144.9 -> 139.6 us, 4096x11008 401.3 -> 391.0, 11008x4096 369.2 ->
+// 353.8; groups of 2 and 4 within 1% of 8; M <= 2048 unchanged.
+constexpr int kPrefillGroupM = 8;
+static int prefill_group_m(int mtiles) { return mtiles <= kPrefillGroupM ? mtiles : kPrefillGroupM; }
+
 template <int MTW, int CG, int GPC, int W>
 static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
   using T = Tile<MTW, CG, GPC, W>;
@@ -462,7 +479,8 @@ static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, h
   const dim3 grid((unsigned)(((units + 7) / 8) * 8 * mtiles));
   prefill2_kernel<MTW, CG, GPC, W><<<grid, W * 64, 0, stream>>>(
       (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps, a.bias,
-      a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles, real_splits);
+      a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles, real_splits,
+      prefill_group_m(mtiles));
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || real_splits == 1) return e;
   return launch_reduce_planes(part, real_splits, a.M, a.N, a.bias, a.y, a.ldy, a.res, a.ldres,
