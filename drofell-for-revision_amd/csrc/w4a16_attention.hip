@@ -28,7 +28,7 @@
 #include <cfloat>
 
 #include "w4a16_device.h"
-#include "w4a16_internal.h"
+#include "w4a16_attention.h"
 
 namespace dw4 {
 

@@ -12,7 +12,9 @@
 #include <vector>
 
 #include "drofell_w4a16.h"
+#include "w4a16_attention.h"
 #include "w4a16_chain.h"
+#include "w4a16_transpose.h"
 #include "w4a16_internal.h"
 
 namespace {

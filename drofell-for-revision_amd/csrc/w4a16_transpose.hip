@@ -30,7 +30,7 @@
 #include <algorithm>
 
 #include "w4a16_device.h"
-#include "w4a16_internal.h"
+#include "w4a16_transpose.h"
 
 namespace dw4 {
 
