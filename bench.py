@@ -15,8 +15,8 @@ graph and replayed; timing uses HIP events on the replay stream.
 
 Printed JSON line: ``value`` = algorithmic bytes moved per second (GB/s) at
 M=1, ``roofline`` for the decode kernel (the only kernel in the step),
-``prefill`` = the same 56 GEMMs at M=256 in TFLOP/s against the fp16 MFMA
-peak, ``cpu_baseline`` = the reference's CPU dequantise-then-matmul path
+``prefill`` = the same 56 GEMMs at M=256 (the same launch grouping) in
+TFLOP/s against the fp16 MFMA peak, ``cpu_baseline`` = the reference's CPU dequantise-then-matmul path
 (restated with torch CPU ops) on a bounded sample, timed in its dequantise,
 matmul and combined phases.
 """
@@ -628,26 +628,26 @@ def device_info(dev) -> dict:
     return info
 
 
-def grouped_leg(mats, dev, steps: int, warmup: int) -> dict:
-    """The 56 projections of the decode leg with the launches a decoder
-    layer's data flow allows: q, k, v share the layer input (one
+def grouped_leg(mats, dev, steps: int, warmup: int, m: int = 1) -> dict:
+    """The 56 projections of the decode leg at M=m with the launches a
+    decoder layer's data flow allows: q, k, v share the layer input (one
     dw4_gemm_group launch), o alone, gate and up share o's output (one
     launch), down alone -- 4 launches per layer instead of 7.  Same
     matrices, same bytes."""
     import torch
-    from gptq_synth import algorithmic_bytes
+    from gptq_synth import algorithmic_bytes, flops
     from hip_extends.w4a16 import gemm_group
 
     gen = torch.Generator(device=dev)
     gen.manual_seed(13)
-    xs = {k: torch.randn(1, k, device=dev, generator=gen).to(torch.float16)
+    xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.float16)
           for k in sorted({t[1] for t in mats})}
     groups = []
     for li in range(len(mats) // 7):
         w = {name.split("_")[0]: (q4, k, n) for name, k, n, q4 in mats[7 * li:7 * li + 7]}
         for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
             k = w[names[0]][1]
-            outs = [torch.empty(1, w[nm][2], dtype=torch.float16, device=dev) for nm in names]
+            outs = [torch.empty(m, w[nm][2], dtype=torch.float16, device=dev) for nm in names]
             groups.append((xs[k], [w[nm][0] for nm in names], outs))
 
     def one_pass():
@@ -658,12 +658,17 @@ def grouped_leg(mats, dev, steps: int, warmup: int) -> dict:
                 gemm_group(x, q4s, outs)
 
     ms = time_callable(one_pass, steps, warmup, dev)
-    nbytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
+    nbytes = sum(algorithmic_bytes(m, k, n, GROUP, False) for _, k, n, _ in mats)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"decode M=1: {ms * 1e3:.1f} us per step ({len(groups)} launches), {gbs:.1f} GB/s")
-    return {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+    tf = sum(flops(m, k, n) for _, k, n, _ in mats) / (ms * 1e-3) / 1e12
+    if m == 1:
+        log(f"decode M=1: {ms * 1e3:.1f} us per step ({len(groups)} launches), {gbs:.1f} GB/s")
+    else:
+        log(f"prefill M={m}: {ms * 1e3:.1f} us per step ({len(groups)} launches), {tf:.1f} TFLOP/s")
+    return {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "TFLOP/s": round(tf, 2),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "launches_per_step": len(groups),
-            "kernel": "dw4::decode_kernel (item table over q/k/v and gate/up)"}
+            "kernel": ("dw4::decode_kernel (item table over q/k/v and gate/up)" if m == 1 else
+                       "dw4::prefill2_kernel (item table over q/k/v and gate/up)")}
 
 
 def chain_leg(mats, dev, steps: int, warmup: int, layers: int) -> dict:
@@ -925,10 +930,7 @@ def main() -> int:
         crossover(mats, dev, args.steps)
         return 0
     if args.only_prefill:
-        m = args.prefill_m
-        pms, _, _ = time_graph(mats, m, args.steps, args.warmup, dev)
-        tf = sum(flops(m, k, n) for _, k, n, _ in mats) / (pms * 1e-3) / 1e12
-        log(f"prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
+        grouped_leg(mats, dev, args.steps, args.warmup, args.prefill_m)
         return 0
     step_bytes = sum(algorithmic_bytes(1, k, n, GROUP, False) for _, k, n, _ in mats)
     grouped = grouped_leg(mats, dev, args.steps, args.warmup)
@@ -1008,15 +1010,25 @@ def main() -> int:
         result["chain"] = chain_leg(mats, dev, args.steps, args.warmup, args.layers)
 
     if not args.no_prefill:
+        # the same 56 GEMMs at M=256 in the same data-flow launches (q/k/v
+        # and gate/up grouped), and with one launch per projection
         m = args.prefill_m
-        pms, _, _ = time_graph(mats, m, max(5, args.steps // 5), max(2, args.warmup // 5), dev)
-        pflop = sum(flops(m, k, n) for _, k, n, _ in mats)
-        tf = pflop / (pms * 1e-3) / 1e12
-        log(f"prefill M={m}: {pms * 1e3:.1f} us per step, {tf:.1f} TFLOP/s")
+        pg = grouped_leg(mats, dev, max(5, args.steps // 5), max(2, args.warmup // 5), m)
+        pms = pg["us_per_step"] * 1e-3
+        tf = pg["TFLOP/s"]
+        ppms, _, _ = time_graph(mats, m, max(5, args.steps // 5), max(2, args.warmup // 5), dev)
+        ptf = sum(flops(m, k, n) for _, k, n, _ in mats) / (ppms * 1e-3) / 1e12
+        log(f"prefill M={m}, one launch per projection: {ppms * 1e3:.1f} us per step, "
+            f"{ptf:.1f} TFLOP/s")
         result["prefill"] = {"m": m, "value": round(tf, 2), "unit": "TFLOP/s",
                              "ms_per_step": round(pms, 5),
                              "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
-                             "peak": MFMA_FP16_PEAK_TFLOPS, "bound": "mfma"}
+                             "peak": MFMA_FP16_PEAK_TFLOPS, "bound": "mfma",
+                             "launches_per_step": pg["launches_per_step"],
+                             "per_projection_launches": {
+                                 "value": round(ptf, 2), "ms_per_step": round(ppms, 5),
+                                 "frac": round(ptf / MFMA_FP16_PEAK_TFLOPS, 4),
+                                 "launches_per_step": len(mats)}}
 
     if args.sweep:
         # each shape rotates over distinct matrices totalling >= 512 MB, so the

@@ -14,6 +14,7 @@
 #include "drofell_w4a16.h"
 #include "w4a16_attention.h"
 #include "w4a16_chain.h"
+#include "w4a16_prefill.h"
 #include "w4a16_transpose.h"
 #include "w4a16_internal.h"
 
@@ -776,6 +777,21 @@ int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, i
       g.count = count;
       for (int i = 0; i < count; ++i) g.a[i] = args_of(m, x, ldx, &items[i]);
       return status_of(dw4::launch_decode_group(g, plan, static_cast<hipStream_t>(stream)));
+    }
+  }
+  // above 128 rows, matrices of equal N without act-order: one launch of the
+  // LDS-streamed prefill kernel, planned as one matrix of the summed N
+  // (so the tiles fill the CUs as a merged matrix's would), when that plan
+  // needs no K split
+  bool same_n = items[0].perm == nullptr;
+  for (int i = 1; i < count; ++i) same_n = same_n && items[i].n == items[0].n;
+  if (m > 128 && same_n && count > 1) {
+    const dw4::PrefillPlan plan = plan_prefill(m, items[0].k, n_total, 0, 0, false);
+    if (plan.splits == 1) {
+      dw4::GroupArgs g{};
+      g.count = count;
+      for (int i = 0; i < count; ++i) g.a[i] = args_of(m, x, ldx, &items[i]);
+      return status_of(dw4::launch_prefill2_group(g, plan, workspace, static_cast<hipStream_t>(stream)));
     }
   }
   for (int i = 0; i < count; ++i) {

@@ -42,7 +42,7 @@
 #include <stdint.h>
 
 #include "w4a16_device.h"
-#include "w4a16_internal.h"
+#include "w4a16_prefill.h"
 
 namespace dw4 {
 
@@ -112,15 +112,27 @@ struct Tile {
   static_assert(kStrips % kWaves == 0 && kKS * CG == kWaves, "wave roles cover the tile");
 };
 
+// Matrices of one launch: equal K, N and group size, each with its own
+// packed buffers, bias, output and residual.  Column tile t of the launch
+// belongs to matrix t / ntiles_item (tiles never straddle two matrices).
+struct P2Items {
+  const u4* pq[kGroupMax];
+  const uint32_t* pz[kGroupMax];
+  const uint32_t* ps[kGroupMax];
+  const uint16_t* bias[kGroupMax];
+  uint16_t* y[kGroupMax];
+  int64_t ldy[kGroupMax];
+  const uint16_t* res[kGroupMax];
+  int64_t ldres[kGroupMax];
+  int ntiles_item;
+};
+
 }  // namespace
 
 template <int MTW, int CG, int GPC, int W>
 __global__ void __launch_bounds__(W * 64)
-prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
-                const u4* __restrict__ pq, const uint32_t* __restrict__ pz,
-                const uint32_t* __restrict__ ps32, const uint16_t* __restrict__ bias,
-                uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ res,
-                int64_t ldres, float* __restrict__ part, int K, int N, int gs, int G,
+prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const P2Items it,
+                float* __restrict__ part, int K, int N, int gs, int G,
                 int chunks_per_split, int mtiles, int ntiles, int splits, int group_m) {
   using T = Tile<MTW, CG, GPC, W>;
   constexpr int kWaves = W;
@@ -153,8 +165,18 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   const int mtile = first_m + jj % gsz;
   const int unit = (jj / gsz) * 8 + (b & 7);
   if (unit >= ntiles * splits) return;
-  const int ntile = unit % ntiles;
   const int split = unit / ntiles;
+  // the launch's column tile -> (matrix, its column tile); wave-uniform
+  const int item = (unit % ntiles) / it.ntiles_item;
+  const int ntile = unit % ntiles - item * it.ntiles_item;
+  const u4* __restrict__ pq = it.pq[item];
+  const uint32_t* __restrict__ pz = it.pz[item];
+  const uint32_t* __restrict__ ps32 = it.ps[item];
+  const uint16_t* __restrict__ bias = it.bias[item];
+  uint16_t* __restrict__ y = it.y[item];
+  const int64_t ldy = it.ldy[item];
+  const uint16_t* __restrict__ res = it.res[item];
+  const int64_t ldres = it.ldres[item];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -465,22 +487,37 @@ constexpr int kPrefillGroupM = 8;
 static int prefill_group_m(int mtiles) { return mtiles <= kPrefillGroupM ? mtiles : kPrefillGroupM; }
 
 template <int MTW, int CG, int GPC, int W>
-static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, hipStream_t stream) {
+static hipError_t launch_prefill2_cfg(const GroupArgs& g, int splits, void* ws,
+                                      hipStream_t stream) {
   using T = Tile<MTW, CG, GPC, W>;
+  const GemmArgs& a = g.a[0];
   const int mtiles = (a.M + T::kBM - 1) / T::kBM;
-  const int ntiles = (a.N + T::kBN - 1) / T::kBN;
+  P2Items it{};
+  it.ntiles_item = (a.N + T::kBN - 1) / T::kBN;
+  for (int i = 0; i < kGroupMax; ++i) {
+    const GemmArgs& b = g.a[i < g.count ? i : 0];
+    it.pq[i] = reinterpret_cast<const u4*>(b.pq);
+    it.pz[i] = b.pz;
+    it.ps[i] = reinterpret_cast<const uint32_t*>(b.ps);
+    it.bias[i] = b.bias;
+    it.y[i] = b.y;
+    it.ldy[i] = b.ldy;
+    it.res[i] = b.res;
+    it.ldres[i] = b.ldres;
+  }
+  const int ntiles = it.ntiles_item * g.count;
   const int KC = a.K / kChunkK;
   const int cps = (KC + splits - 1) / splits;
   const int real_splits = (KC + cps - 1) / cps;
+  if (real_splits > 1 && g.count != 1) return hipErrorInvalidValue;  // planes of one matrix
   float* part = real_splits > 1
                     ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + kWsHeadBytes)
                     : nullptr;
   const int units = ntiles * real_splits;
   const dim3 grid((unsigned)(((units + 7) / 8) * 8 * mtiles));
   prefill2_kernel<MTW, CG, GPC, W><<<grid, W * 64, 0, stream>>>(
-      (const _Float16*)a.x, a.ldx, a.M, (const u4*)a.pq, a.pz, (const uint32_t*)a.ps, a.bias,
-      a.y, a.ldy, a.res, a.ldres, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles, real_splits,
-      prefill_group_m(mtiles));
+      (const _Float16*)a.x, a.ldx, a.M, it, part, a.K, a.N, a.gs, a.G, cps, mtiles, ntiles,
+      real_splits, prefill_group_m(mtiles));
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || real_splits == 1) return e;
   return launch_reduce_planes(part, real_splits, a.M, a.N, a.bias, a.y, a.ldy, a.res, a.ldres,
@@ -488,17 +525,32 @@ static hipError_t launch_prefill2_cfg(const GemmArgs& a, int splits, void* ws, h
 }
 
 template <int MTW, int CG, int W>
-static hipError_t launch_prefill2_tile(const GemmArgs& a, int splits, void* ws,
+static hipError_t launch_prefill2_tile(const GroupArgs& a, int splits, void* ws,
                                        hipStream_t stream) {
-  const int gpc = a.gs >= kChunkK ? 1 : kChunkK / a.gs;
+  const int gpc = a.a[0].gs >= kChunkK ? 1 : kChunkK / a.a[0].gs;
   if (gpc == 1) return launch_prefill2_cfg<MTW, CG, 1, W>(a, splits, ws, stream);
   if (gpc == 2) return launch_prefill2_cfg<MTW, CG, 2, W>(a, splits, ws, stream);
   return launch_prefill2_cfg<MTW, CG, 4, W>(a, splits, ws, stream);
 }
 
-hipError_t launch_prefill2(const GemmArgs& a, const PrefillPlan& plan, void* ws,
+hipError_t launch_prefill2(const GemmArgs& one, const PrefillPlan& plan, void* ws,
                            hipStream_t stream) {
-  if (a.perm != nullptr) return hipErrorInvalidValue;  // x must already be in packed row order
+  GroupArgs g{};
+  g.count = 1;
+  g.a[0] = one;
+  return launch_prefill2_group(g, plan, ws, stream);
+}
+
+hipError_t launch_prefill2_group(const GroupArgs& a, const PrefillPlan& plan, void* ws,
+                                 hipStream_t stream) {
+  if (a.count < 1 || a.count > kGroupMax) return hipErrorInvalidValue;
+  for (int i = 0; i < a.count; ++i) {
+    const GemmArgs& b = a.a[i];
+    // x must already be in packed row order; one x, K, N and group size
+    if (b.perm != nullptr || b.x != a.a[0].x || b.ldx != a.a[0].ldx || b.M != a.a[0].M ||
+        b.K != a.a[0].K || b.N != a.a[0].N || b.gs != a.a[0].gs)
+      return hipErrorInvalidValue;
+  }
   if (plan.waves == 4) {  // two workgroups per CU
     if (plan.bm == 64 && plan.bn == 128) return launch_prefill2_tile<2, 2, 4>(a, plan.splits, ws, stream);
     if (plan.bm == 32 && plan.bn == 128) return launch_prefill2_tile<1, 2, 4>(a, plan.splits, ws, stream);

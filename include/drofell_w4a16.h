@@ -267,8 +267,10 @@ typedef struct dw4_item {
 /* y_i = x @ W_i (+ bias_i) for 1..4 matrices that share x, k and
  * group_size (with perm on all or on none).  For m <= 32 where
  * DW4_PATH_AUTO would take the decode kernel for the summed N, one launch
- * covers every strip of every matrix; otherwise the matrices run one after
- * another as dw4_gemm does.  workspace: at least
+ * covers every strip of every matrix; for m > 128 with matrices of equal n
+ * and no perm, one prefill launch covers every column tile of every matrix
+ * when the plan for the summed N needs no K split; otherwise the matrices
+ * run one after another as dw4_gemm does.  workspace: at least
  * dw4_workspace_size of each item. */
 int dw4_gemm_group(int count, const dw4_item* items, int m, const uint16_t* x, int64_t ldx,
                    void* workspace, size_t workspace_bytes, void* stream);

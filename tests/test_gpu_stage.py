@@ -110,6 +110,44 @@ def test_gemm_group_mixed_widths(hip_device):
             check(o, gptq.gemm_ref(x.numpy(), w), f"mixed M={m} item {i}")
 
 
+@pytest.mark.parametrize("case", ["qkv", "gate_up", "partial_tiles", "split_fallback"])
+def test_gemm_group_prefill(hip_device, case):
+    """Above 128 rows, matrices of equal N in one LDS-streamed prefill launch
+    (planned for the summed N), each with its own output and bias; the
+    plans that would split K run the matrices one after another."""
+    import ctypes
+
+    from hip_extends.w4a16 import _item
+    k, n, count, ms = {"qkv": (4096, 4096, 3, (129, 200, 256, 300, 512)),
+                       "gate_up": (4096, 11008, 2, (256, 384)),
+                       "partial_tiles": (2048, 1040, 2, (160, 256)),
+                       "split_fallback": (11008, 4096, 2, (256,))}[case]
+    lws = [layer_w(k, n, 128, 500 + i, False) for i in range(count)]
+    q4s = build([lw[0] for lw in lws], hip_device, max_m=max(ms))
+    gen = torch.Generator().manual_seed(3)
+    bias = (torch.randn(n, generator=gen) * 0.5).to(torch.float16)
+    ws = q4s[0].cache.workspace
+    lib = _lib.load()
+    for m in ms:
+        say(f"group prefill {case} M={m}")
+        x = make_x(m, k, seed=700 + m)
+        xd = x.to(hip_device)
+        outs = [torch.full((m, n), float("nan"), dtype=torch.float16, device=hip_device)
+                for _ in range(count)]
+        items = (_lib.Item * count)(*[_item(q, o) for q, o in zip(q4s, outs)])
+        bd = bias.to(hip_device)
+        items[1].bias = bd.data_ptr()  # the second matrix carries a bias
+        st = lib.dw4_gemm_group(count, items, m, xd.data_ptr(), xd.stride(0), ws.data_ptr(),
+                                ws.numel(), torch.cuda.current_stream(hip_device).cuda_stream)
+        assert st == _lib.DW4_OK, _lib.load().dw4_strerror(st)
+        torch.cuda.synchronize()
+        for i, (o, (_, w)) in enumerate(zip(outs, lws)):
+            ref = gptq.gemm_ref(x.numpy(), w)
+            if i == 1:
+                ref = ref + bias.float().numpy()[None, :]
+            check(o, ref, f"group prefill {case} M={m} item {i}")
+
+
 def _silu_mul_call(dev, x, gq, uq, h, tg=None, tu=None):
     from hip_extends.w4a16 import _item
     ig, iu = _item(gq, tg), _item(uq, tu)
