@@ -1084,6 +1084,10 @@ int dw4_chain_prepare(int count, const dw4_chain_link* links, int m, void* chain
     p.max_groups = std::max(p.max_groups, links[i].k / links[i].group_size);
     const int strips = links[i].n / kStripN;
     p.max_strips = std::max(p.max_strips, (strips + p.workgroups - 1) / p.workgroups);
+    // the kernel deals strips to workgroups with floor(r * strips / W) by a
+    // multiplier, exact while r * strips * W < 2^32 (r <= W)
+    if ((uint64_t)p.workgroups * p.workgroups * (uint64_t)strips >= (1ull << 32))
+      return DW4_ERR_UNSUPPORTED;
   }
   if (!dw4::plan_chain(p)) return DW4_ERR_UNSUPPORTED;
 
