@@ -24,6 +24,12 @@
 
 namespace dw4 {
 
+// Relaxed agent-scope load (sc1, past the XCD's L2) of a partial another
+// workgroup wrote through with an agent-scope store.
+__device__ __forceinline__ float load_agent(float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // Load-time repack
 // ---------------------------------------------------------------------------
@@ -365,18 +371,18 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   // counter for the next call.  No workgroup ever waits for another.
   //
   // Partials are written as relaxed agent-scope atomic stores, which gfx950
-  // performs write-through (sc1): they leave no dirty L2 lines, so thread
-  // 0's agent-scope release -- an L2 write-back -- has almost nothing to
-  // write (with plain stores it had to flush every workgroup's partials and
-  // cost several microseconds).  Layout per split plane (mtiles*ntiles*BM*BN
-  // floats): [tile][mt*S + si][element e of the lane's float4][256 threads],
-  // so each store instruction covers 256 contiguous bytes per wave.
-  // Ordering is the usual publish/consume pattern: every wave waits for its
-  // own stores to complete, the barrier then orders all of them before
-  // thread 0's release and counter increment (a release covers only the
-  // issuing wave's operations, and s_barrier does not wait for memory); the last
-  // arriver's acquire (then the barrier) orders the other splits' partials
-  // before its loads.  Fences run once per workgroup.
+  // performs write-through (sc1), and the last arriver reads them back with
+  // relaxed agent-scope loads (sc1), which read past the XCD's L2.  Every
+  // wave waits for its own stores to complete (s_barrier does not wait for
+  // memory), then the barrier precedes thread 0's counter increment, so
+  // the increment happens after every partial store of the workgroup has
+  // been performed, and the last arriver's loads are issued after it has
+  // seen the count.  No release or acquire fence: on gfx950 those write
+  // back or invalidate the whole L2 of the XCD, under the feet of every
+  // other workgroup streaming through it.  Layout per split plane
+  // (mtiles*ntiles*BM*BN floats): [tile][mt*S + si][element e of the
+  // lane's float4][256 threads], so each store instruction covers 256
+  // contiguous bytes per wave.
   const int tile_id = mtile * ntiles + ntile;
   const size_t plane = (size_t)mtiles * ntiles * (MT2 * S) * 1024;  // floats per split
   const size_t tbase = (size_t)tile_id * (MT2 * S) * 1024 + tid;
@@ -392,11 +398,9 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   __shared__ int last_arrival;
   __syncthreads();
   if (tid == 0) {
-    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELEASE,
+    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
-    const int last = before == splits - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    last_arrival = last;
+    last_arrival = before == splits - 1;
   }
   __syncthreads();
   if (!last_arrival) return;
@@ -413,9 +417,10 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
     for (int mt = 0; mt < MT2; ++mt)
 #pragma unroll
       for (int si = 0; si < S; ++si) {
-        const float* src = part + (size_t)sp * plane + tbase + (mt * S + si) * 1024;
+        float* src = part + (size_t)sp * plane + tbase + (mt * S + si) * 1024;
         t[mt][si] = sp == split ? f4{acc[mt][si][0], acc[mt][si][1], acc[mt][si][2], acc[mt][si][3]}
-                                : f4{src[0], src[256], src[512], src[768]};
+                                : f4{load_agent(src), load_agent(src + 256),
+                                     load_agent(src + 512), load_agent(src + 768)};
       }
 #pragma unroll
     for (int mt = 0; mt < MT2; ++mt)
@@ -708,11 +713,9 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
   __shared__ int last_arrival;
   __syncthreads();
   if (tid == 0) {
-    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELEASE,
+    const int before = __hip_atomic_fetch_add(&counters[tile_id], 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
-    const int last = before == splits - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    last_arrival = last;
+    last_arrival = before == splits - 1;
   }
   __syncthreads();
   if (!last_arrival) return;
@@ -731,14 +734,14 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
         for (int p = 0; p < P; ++p) sum[mt][p] += acc[mt][p];
       continue;
     }
-    const float* src = part + (size_t)sp2 * plane + tbase;
+    float* src = part + (size_t)sp2 * plane + tbase;
 #pragma unroll
     for (int mt = 0; mt < MT3; ++mt)
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         f16v t;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) t[i] = src[((mt * P + p) * 16 + i) * 256];
+        for (int i = 0; i < 16; ++i) t[i] = load_agent(src + ((mt * P + p) * 16 + i) * 256);
         sum[mt][p] += t;
       }
   }
