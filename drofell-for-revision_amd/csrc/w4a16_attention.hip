@@ -109,12 +109,6 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
     }
     return;
   }
-  for (int i = tid; i < G * HS; i += (W * 64)) {
-    const int g = i / HS, d = i % HS;
-    qs[i] = scale * (float)as_h(query[(size_t)seq * q_stride + (size_t)(h0 + g) * HS + d]);
-  }
-  __syncthreads();
-
   const int32_t* btab = block_tables + (size_t)seq * max_blocks + t0 / BS;
   const int nb = (nt + BS - 1) / BS;
   const int nbw = wave < nb ? (nb - wave + W - 1) / W : 0;  // this wave's blocks
@@ -162,6 +156,16 @@ paged_attention_kernel(const uint16_t* __restrict__ query, int64_t q_stride,
       load_k(u, u);
       load_v(u, u);
     }
+  // The query is staged after the first blocks' key and value loads went
+  // out (each behind its block-table and block-pointer loads), so its own
+  // load overlaps theirs; the barrier that publishes it waits only for the
+  // LDS stores, and the key/value loads stay in flight across it (a
+  // __syncthreads would wait for them).
+  for (int i = tid; i < G * HS; i += (W * 64)) {
+    const int g = i / HS, d = i % HS;
+    qs[i] = scale * (float)as_h(query[(size_t)seq * q_stride + (size_t)(h0 + g) * HS + d]);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // q . k
   auto qk = [&](int slot, int i) {
