@@ -122,6 +122,12 @@ CASES = [
     ([129, 1, 800, 300], 384, 48, 64, 16, False),
     ([5, 900, 333, 64, 1, 2], 128, 32, 112, 16, False),
     ([1, 17, 1024, 511, 512, 33, 300, 64, 100], 64, 16, 128, 16, False),
+    # the 16-wave form past 32 blocks, where a wave's third (and fourth)
+    # block reloads a register slot after the first blocks' q . k and p . v:
+    # the 7B stage's shape as its contexts grow past 512 (ALiBi added), and
+    # 4 query heads per kv head at head size 64
+    ([640, 513, 600, 576, 1, 530, 700, 520], 32, 32, 128, 16, True),
+    ([1000, 520, 3, 777], 160, 40, 64, 16, False),
 ]
 
 
