@@ -412,6 +412,57 @@ int dw4_gemm(int m, int k, int n, int group_size, const uint16_t* x, int64_t ldx
                        packed_scales, perm, bias, y, ldy, workspace, workspace_bytes, stream);
 }
 
+static_assert(dw4::kBf16MaxM == DW4_BF16_MAX_M, "bf16 decode limit");
+
+int dw4_gemm_bf16(int m, int k, int n, int group_size, const uint16_t* x, int64_t ldx,
+                  const int32_t* packed_qweight, const int32_t* packed_zeros,
+                  const uint16_t* packed_scales, const int32_t* perm, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  const int st = check_shape(k, n, group_size);
+  if (st != DW4_OK) return st;
+  if (m < 0) return DW4_ERR_INVALID_ARG;
+  if (m == 0) return DW4_OK;
+  if (m > DW4_BF16_MAX_M) return DW4_ERR_UNSUPPORTED;
+  if (!x || !packed_qweight || !packed_zeros || !packed_scales || !y) return DW4_ERR_INVALID_ARG;
+  if (ldx < k || ldy < n) return DW4_ERR_INVALID_ARG;
+  if (!aligned16(x) || (ldx % 8) != 0 || !aligned16(packed_qweight)) return DW4_ERR_MISALIGNED;
+  // the register-fed kernel addresses rows of x with 32-bit offsets
+  if (!rows_fit_i32(m, ldx, k)) return DW4_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dw4::GemmArgs a;
+  a.M = m;
+  a.K = k;
+  a.N = n;
+  a.gs = group_size;
+  a.G = k / group_size;
+  a.x = x;
+  a.ldx = ldx;
+  a.pq = reinterpret_cast<const uint32_t*>(packed_qweight);
+  a.pz = reinterpret_cast<const uint32_t*>(packed_zeros);
+  a.ps = packed_scales;
+  a.perm = perm;
+  a.bias = bias;
+  a.y = y;
+  a.ldy = ldy;
+  a.res = nullptr;
+  a.ldres = 0;
+  // act-order: x gathered into the packed row order once where the
+  // workspace has room (2-byte elements: the fp16 gather serves bf16)
+  if (perm != nullptr && workspace != nullptr && aligned16(workspace)) {
+    const size_t off = dw4::gather_offset(0);
+    if (workspace_bytes >= off + dw4::gather_bytes(m, k)) {
+      uint16_t* xs = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(workspace) + off);
+      const int e = status_of(dw4::launch_gather_rows(x, ldx, perm, xs, k, m, s));
+      if (e != DW4_OK) return e;
+      a.x = xs;
+      a.ldx = k;
+      a.perm = nullptr;
+    }
+  }
+  return status_of(dw4::launch_decode_reg_bf16(a, dw4::plan_decode_bf16(k, n, cu_count()), s));
+}
+
 int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,
                 const int32_t* packed_zeros, const uint16_t* packed_scales, const int32_t* perm,
                 uint16_t* w, int64_t ldw, void* stream) {

@@ -369,8 +369,20 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
 // ---------------------------------------------------------------------------
 
 // MODE: kRegSingle (one matrix, item 0 read directly), kRegGroup (several
-// matrices, item looked up per workgroup) or kRegPair (gate/up, above).
-constexpr int kRegSingle = 0, kRegGroup = 1, kRegPair = 2;
+// matrices, item looked up per workgroup), kRegPair (gate/up, above) or
+// kRegBf16 (one matrix, bf16 activations and output, unsplit).
+//
+// bf16 mode: the B operands are the exact bf16 values 128 + q (no zero
+// subtraction per fragment) on v_mfma_f32_16x16x32_bf16, and per group
+//   sum_k x (q - z) = sum_k x (128 + q) - (128 + z) sum_k x,
+// where sum_k x comes from one more MFMA per k-step against a bf16 ones
+// operand (the row sums land in the accumulator layout, replicated over the
+// columns); the scale is applied per group in fp32 as in the fp16 modes.
+// Output bf16(sum) (+ bias in bf16 after the rounding, as the dense route's
+// `y += bias`).  The weights are the fp16 checkpoint's s (q - z) unrounded,
+// so the product is within rounding of the reference's bf16 route
+// (reconstruct bf16(fp16(s (q - z))), then a bf16 GEMM).
+constexpr int kRegSingle = 0, kRegGroup = 1, kRegPair = 2, kRegBf16 = 3;
 
 
 template <int MT, int WAVES, int U, int SS, int GPC, bool ACT, int MODE>
@@ -378,6 +390,7 @@ __global__ void __launch_bounds__(WAVES * 64)
 decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d, int K,
                   int gs, int G, int cps, float* __restrict__ part) {
   constexpr bool PAIR = MODE == kRegPair;
+  constexpr bool BF = MODE == kRegBf16;
   static_assert(!PAIR || SS == 2, "a pair workgroup holds one strip of each matrix");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int T = WAVES * 64;
@@ -470,7 +483,8 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   for (int ss = 0; ss < SS; ++ss)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) tot[ss][mt] = f4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t magic = kMagic;
+  const uint32_t magic = BF ? kMagicBf16 : kMagic;
+  const u4 ones_bf16 = u4{kOnesBf16, kOnesBf16, kOnesBf16, kOnesBf16};
   auto consume = [&](int slot_u) {
     if constexpr (LX) {  // the slot's registers go out in load order, come back in operand order
 #pragma unroll
@@ -481,6 +495,40 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int t = 0; t < 4; ++t) ab[slot_u][mt][t] = *(const h8*)(xs + mt * 4096 + xoff_r[t]);
+    }
+    if constexpr (BF) {
+#pragma unroll
+      for (int gl = 0; gl < GPC; ++gl) {
+        f4 rsum[MT];  // sum of the group's x per row, in every column
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) rsum[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int tt = 0; tt < SPG; ++tt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            rsum[mt] = mfma16_bf16(ab[slot_u][mt][gl * SPG + tt], ones_bf16, rsum[mt]);
+#pragma unroll
+        for (int ss = 0; ss < SS; ++ss) {
+          const float zc = (float)(128u + ((zb[slot_u][ss][gl] >> zsh) & 15u) + 1u);
+          const float sc = (float)as_h((uint16_t)(sb[slot_u][ss][gl] >> hsh));
+          f4 acc[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int tt = 0; tt < SPG; ++tt) {
+            const int t = gl * SPG + tt;
+            const u4 b = biased8_bf16(qb[slot_u][ss][t], magic);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma16_bf16(ab[slot_u][mt][t], b, acc[mt]);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              tot[ss][mt][e] = fmaf(sc, fmaf(-zc, rsum[mt][e], acc[mt][e]), tot[ss][mt][e]);
+        }
+      }
+      return;
     }
 #pragma unroll
     for (int ss = 0; ss < SS; ++ss)
@@ -583,6 +631,12 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
       if (m >= M || st >= NS) continue;
       const int L = lhi * 16 + llo;
       const int n = st * kStripN + llo;
+      if constexpr (BF) {
+        uint16_t o = bf16_rne(wave_sum(sm, L, r));
+        if (bias != nullptr) o = bf16_rne(bf16_f32(o) + bf16_f32(bias[n]));
+        y[(size_t)m * ldy + n] = o;
+        continue;
+      }
       if (MODE == kRegSingle && gridDim.y > 1) {  // this split's fp32 plane
         part[((size_t)split * M + m) * N + n] = wave_sum(sm, L, r);
         continue;
@@ -765,6 +819,19 @@ hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, float* par
   if (M <= 48) return launch_decode_reg_m<3>(g, p, sp, stream);
   if (M <= 64) return launch_decode_reg_m<4>(g, p, sp, stream);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_reg_bf16(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
+  if (a.M < 1 || a.M > kBf16MaxM || !p.reg || p.splits != 1 || a.res != nullptr)
+    return hipErrorInvalidValue;
+  GroupArgs g{};
+  g.count = 1;
+  g.a[0] = a;
+  const RegSplit sp{1, a.K / kChunkK, nullptr};
+  if (p.waves == 16) return launch_decode_reg_w<1, 16, 1, kRegBf16>(g, sp, stream);
+  if (p.waves != 8) return hipErrorInvalidValue;
+  return p.ss == 2 ? launch_decode_reg_w<1, 8, 2, kRegBf16>(g, sp, stream)
+                   : launch_decode_reg_w<1, 8, 1, kRegBf16>(g, sp, stream);
 }
 
 hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipStream_t stream) {

@@ -23,14 +23,19 @@ __device__ __forceinline__ _Float16 as_h(uint16_t u) { return __builtin_bit_cast
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ h2 splat2(_Float16 v) { return h2{v, v}; }
 
-// (a & mask) | magic in one VALU instruction.  Written out because the
-// compiler splits it into two when both constants are literals (a gfx9 VOP3
-// instruction cannot encode two literals); here the mask comes from an SGPR
-// and the magic value from a VGPR.
+// (a & mask) | magic in one v_and_or_b32 (mask in an SGPR, magic in a
+// VGPR).  magic first passes through an empty assembly statement that hides
+// its constant value: with both constants known the compiler would emit two
+// instructions (a gfx9 VOP3 instruction cannot encode literals).  The
+// v_and_or_b32 itself stays the compiler's, so its hazard recognizer sees the
+// register write and keeps the wait states the matrix cores need around it
+// (an MFMA reading a VALU result; a VALU overwriting the SrcC or the
+// destination of an MFMA in flight).  Written as assembly, the instruction
+// was invisible to it: results then fed MFMAs, or overwrote an in-flight
+// MFMA's SrcC, closer than those wait states.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
-  return r;
+  asm("" : "+v"(magic));
+  return (a & mask) | magic;
 }
 
 // The 8 rows of one packed word, minus the effective zero, as exact fp16
@@ -70,6 +75,37 @@ __device__ __forceinline__ void wait_own_stores() {
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// bf16 operands: the same 16 bytes per lane as h8, read as eight bf16.
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4 mfma16_bf16(h8 a, u4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a),
+                                                  __builtin_bit_cast(b8, b), c, 0, 0, 0);
+}
+
+constexpr uint32_t kMagicBf16 = 0x43004300u;  // bf16 128.0 in both halves
+constexpr uint32_t kOnesBf16 = 0x3F803F80u;   // bf16 1.0 in both halves
+
+// The 8 rows of one packed word as the bf16 values 128 + q, in row order
+// (even rows of a nibble pair in the low half-word, as centered8 reads
+// them).  bf16 keeps 7 mantissa bits, so OR-ing a nibble into the pattern
+// of 128.0 gives 128 + q exactly; each pair is shifted down to bits 0-3 of
+// its half-words first (a nibble at bits 4-7 would reach the exponent).
+__device__ __forceinline__ u4 biased8_bf16(uint32_t w, uint32_t magic) {
+  return u4{and_or(w, 0x000F000Fu, magic), and_or(w >> 4, 0x000F000Fu, magic),
+            and_or(w >> 8, 0x000F000Fu, magic), and_or(w >> 12, 0x000F000Fu, magic)};
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet), and back.
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bf16_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 
 typedef float f16v __attribute__((ext_vector_type(16)));

@@ -262,6 +262,22 @@ hipError_t launch_decode_group(const GroupArgs& g, const DecodePlan& p, hipStrea
 // and equal perm (gate, up): one register-fed launch, workgroup s holding strip s of both.
 constexpr int kPairMaxM = 32;  // largest M of launch_decode_pair
 hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipStream_t stream);
+// bf16 activations and output, 1 <= M <= kBf16MaxM, one matrix: the
+// register-fed kernel's bf16 mode, unsplit (one row tile; two strips per
+// workgroup where the strips fill the CUs twice, 16 waves where one strip
+// per workgroup leaves every wave two chunks or more).
+constexpr int kBf16MaxM = 16;  // DW4_BF16_MAX_M of the public header
+inline DecodePlan plan_decode_bf16(int k, int n, int cus) {
+  const int kc = k / kChunkK;
+  const int strips = n / kStripN;
+  DecodePlan r{1, kc, 8, 0};
+  r.reg = true;
+  r.ss = (strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
+  if (r.ss == 1 && strips <= cus && kc >= 32) r.waves = 16;
+  r.smem = (size_t)r.waves * r.ss * 64 * 16;
+  return r;
+}
+hipError_t launch_decode_reg_bf16(const GemmArgs& a, const DecodePlan& p, hipStream_t stream);
 // Elementwise h = fp16(silu(g) * u) over [m, n] (row strides ldg, ldu, ldh).
 hipError_t launch_silu_mul(const uint16_t* g, int64_t ldg, const uint16_t* u, int64_t ldu,
                            uint16_t* h, int64_t ldh, int m, int n, hipStream_t stream);

@@ -78,6 +78,8 @@ SIGNATURES = {
     "dw4_repack": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _P, _P, _P, _P, _P, _P, _P, _P]),
     "dw4_gemm": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64,
                             _P, _P, _P, _P, _P, _P, _c.c_int64, _P, _c.c_size_t, _P]),
+    "dw4_gemm_bf16": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _P, _c.c_int64,
+                                 _P, _P, _P, _P, _P, _P, _c.c_int64, _P, _c.c_size_t, _P]),
     "dw4_gemm_path": (_c.c_int, [_c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int, _c.c_int,
                                  _P, _c.c_int64, _P, _P, _P, _P, _P, _P, _c.c_int64,
                                  _P, _c.c_size_t, _P]),
@@ -124,7 +126,8 @@ SIGNATURES = {
     "dw4_gemm_chain": (_c.c_int, [_CPP, _P, _P]),
     "dw4_chain_timed_out": (_c.c_int, [_P, _c.POINTER(_c.c_int)]),
 }
-ABI_VERSION = 9
+ABI_VERSION = 10
+BF16_MAX_M = 16  # DW4_BF16_MAX_M
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -14,6 +14,10 @@
  *                    q4_matmul_blas_v2 (entry.cpp:303-340), marlin_gemm
  *                    (ops_registration.cpp:43-49); the M-based dispatch of
  *                    Q4MatrixV2.matmul (cuda_extends/exllama.py:492-526)
+ *   dw4_gemm_bf16    q4_matmul_blas_v2 with bfloat16 (entry.cpp:303-340: a
+ *                    bf16 reconstruction, then a bf16 GEMM), the route of
+ *                    Q4MatrixV2.matmul for bf16 x (cuda_extends/exllama.py:492-526),
+ *                    for 1 <= M <= DW4_BF16_MAX_M
  *   dw4_dequant      q4_to_half_matrix_v2 (entry.cpp:79-91) and
  *                    marlin_dequant_into (cuda_extends/marlin/marlin_dequant.cu:97-172)
  *   dw4_reshape_and_cache / dw4_restore_from_cache / dw4_paged_attention
@@ -100,7 +104,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 9
+#define DW4_ABI_VERSION 10
 
 enum {
   DW4_OK = 0,
@@ -167,6 +171,25 @@ int dw4_gemm(int m, int k, int n, int group_size,
              const uint16_t* packed_scales, const int32_t* perm,
              const uint16_t* bias, uint16_t* y, int64_t ldy,
              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device: y[M, N] = bf16(x[M, K] @ W) (+ bias[N] in bf16, added after that
+ * rounding) for bf16 activations x and a bf16 output y, 1 <= m <=
+ * DW4_BF16_MAX_M; larger m returns DW4_ERR_UNSUPPORTED (the caller keeps
+ * the dense route: dw4_dequant_bf16, then a bf16 library GEMM).  One
+ * register-fed decode launch on bf16 matrix cores, fp32 accumulation over
+ * the exact integers q - z and the fp16 scales applied per group in fp32, so
+ * the product is within rounding of the dense route's (whose weight is
+ * rounded to bf16 first).  Same buffers, alignment and perm as dw4_gemm;
+ * act-order calls use the workspace of dw4_workspace_size(m, ...) for x
+ * gathered into the packed row order when it has room (otherwise every
+ * workgroup gathers, same result); no K split. */
+#define DW4_BF16_MAX_M 16
+int dw4_gemm_bf16(int m, int k, int n, int group_size,
+                  const uint16_t* x, int64_t ldx,
+                  const int32_t* packed_qweight, const int32_t* packed_zeros,
+                  const uint16_t* packed_scales, const int32_t* perm,
+                  const uint16_t* bias, uint16_t* y, int64_t ldy,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* dw4_gemm with an explicit path (DW4_PATH_*) and prefill split-K factor
  * (0 = automatic); for tests and benchmarks. */

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 9
+    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 10
 
 
 def test_strerror_names_every_status():
@@ -76,6 +76,31 @@ def test_shape_validation_codes():
                            None) == _lib.DW4_ERR_INVALID_ARG
     assert lib.dw4_gemm_path(7, 0, 1, 128, 64, 128, None, 128, None, None, None, None, None,
                              None, 64, None, 0, None) == _lib.DW4_ERR_INVALID_ARG
+
+
+def test_gemm_bf16_validates_before_launch():
+    """dw4_gemm_bf16 (bf16 activations, the register-fed kernel's bf16 mode)
+    rejects every malformed call before anything reaches a device; the fake,
+    aligned addresses are never dereferenced."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    odd = ctypes.c_void_p((1 << 20) + 8)
+
+    def call(m, k=4096, n=4096, g=128, x=fake, ldx=4096, ldy=4096, y=fake):
+        return lib.dw4_gemm_bf16(m, k, n, g, x, ldx, fake, fake, fake, None, None, y, ldy,
+                                 None, 0, None)
+
+    assert call(0) == _lib.DW4_OK  # empty input: nothing to do
+    assert call(-1) == _lib.DW4_ERR_INVALID_ARG
+    assert call(_lib.BF16_MAX_M + 1) == _lib.DW4_ERR_UNSUPPORTED  # the dense route's M
+    assert call(1, k=96, g=32) == _lib.DW4_ERR_UNSUPPORTED
+    assert call(1, x=None) == _lib.DW4_ERR_INVALID_ARG
+    assert call(1, y=None) == _lib.DW4_ERR_INVALID_ARG
+    assert call(1, ldx=4088) == _lib.DW4_ERR_INVALID_ARG
+    assert call(1, ldy=4000) == _lib.DW4_ERR_INVALID_ARG
+    assert call(1, x=odd) == _lib.DW4_ERR_MISALIGNED
+    assert call(2, ldx=4100) == _lib.DW4_ERR_MISALIGNED
+    assert call(2, ldx=(1 << 31) + 8) == _lib.DW4_ERR_UNSUPPORTED  # 32-bit row offsets
 
 
 def test_decode_rejects_rows_beyond_32bit_offsets():
