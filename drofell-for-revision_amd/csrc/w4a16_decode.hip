@@ -552,6 +552,41 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
       }
   };
 
+  // Epilogue output idx (< SS * MT * 256) -> row m, strip st, column n.
+  auto epi_pos = [&](int idx, int& m, int& st, int& n) {
+    const int sm = idx >> 8;  // ss * MT + mt
+    const int ss = sm / MT;
+    const int mt = sm - ss * MT;
+    m = mt * 16 + ((idx >> 6) & 3) * 4 + ((idx >> 4) & 3);
+    st = s0 + ss;
+    n = st * kStripN + (idx & 15);
+  };
+  // One row tile: the epilogue's bias and residual values are loaded before
+  // the weight stream, so their latency hides under it instead of adding a
+  // memory round trip after the cross-wave sum (the residual may be y
+  // itself: each element is read and later written by the same thread).
+  // Wider tiles load them in the epilogue (the registers would spill).
+  constexpr bool PRE = !PAIR && MT == 1;
+  constexpr int EPI = (SS * MT * 256 + T - 1) / T;  // epilogue outputs per thread
+  uint16_t epi_bias[PRE ? EPI : 1], epi_res[PRE ? EPI : 1];
+  if constexpr (PRE) {
+    const uint16_t* __restrict__ bias = pick(d.bias, item);
+    const uint16_t* __restrict__ res = pick(d.res, item);
+    const int64_t ldres = pick(d.ldres, item);
+    const bool planes = MODE == kRegSingle && gridDim.y > 1;  // the reduce adds them
+#pragma unroll
+    for (int e = 0; e < EPI; ++e) {
+      epi_bias[e] = 0;
+      epi_res[e] = 0;
+      const int idx = tid + e * T;
+      int m, st, n;
+      epi_pos(idx, m, st, n);
+      if (planes || idx >= SS * MT * 256 || m >= M || st >= NS) continue;
+      if (bias != nullptr) epi_bias[e] = bias[n];
+      if (res != nullptr) epi_res[e] = res[(size_t)m * ldres + n];
+    }
+  }
+
   // ring: the host gives every wave at least U chunks when U >= 2
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -619,32 +654,60 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
     const uint16_t* __restrict__ res = pick(d.res, item);
     const int64_t ldres = pick(d.ldres, item);
     const int N = NS * kStripN;
-    for (int idx = tid; idx < SS * MT * 256; idx += T) {
-      const int sm = idx >> 8;  // ss * MT + mt
-      const int ss = sm / MT;
-      const int mt = sm - ss * MT;
-      const int llo = idx & 15;
-      const int r = (idx >> 4) & 3;
-      const int lhi = (idx >> 6) & 3;
-      const int m = mt * 16 + lhi * 4 + r;
-      const int st = s0 + ss;
-      if (m >= M || st >= NS) continue;
-      const int L = lhi * 16 + llo;
-      const int n = st * kStripN + llo;
-      if constexpr (BF) {
-        uint16_t o = bf16_rne(wave_sum(sm, L, r));
-        if (bias != nullptr) o = bf16_rne(bf16_f32(o) + bf16_f32(bias[n]));
-        y[(size_t)m * ldy + n] = o;
-        continue;
+    if constexpr (PRE) {  // one row tile: bias and residual prefetched
+#pragma unroll
+      for (int e = 0; e < EPI; ++e) {
+        const int idx = tid + e * T;
+        if (idx >= SS * MT * 256) break;
+        int m, st, n;
+        epi_pos(idx, m, st, n);
+        if (m >= M || st >= NS) continue;
+        const int sm = idx >> 8;
+        const int L = ((idx >> 6) & 3) * 16 + (idx & 15);
+        const int r = (idx >> 4) & 3;
+        if constexpr (BF) {
+          uint16_t o = bf16_rne(wave_sum(sm, L, r));
+          if (bias != nullptr) o = bf16_rne(bf16_f32(o) + bf16_f32(epi_bias[e]));
+          y[(size_t)m * ldy + n] = o;
+          continue;
+        }
+        if (MODE == kRegSingle && gridDim.y > 1) {  // this split's fp32 plane
+          part[((size_t)split * M + m) * N + n] = wave_sum(sm, L, r);
+          continue;
+        }
+        _Float16 out = (_Float16)wave_sum(sm, L, r);
+        if (bias != nullptr) out = out + as_h(epi_bias[e]);
+        if (res != nullptr) out = out + as_h(epi_res[e]);
+        y[(size_t)m * ldy + n] = h_bits(out);
       }
-      if (MODE == kRegSingle && gridDim.y > 1) {  // this split's fp32 plane
-        part[((size_t)split * M + m) * N + n] = wave_sum(sm, L, r);
-        continue;
+    } else {
+      for (int idx = tid; idx < SS * MT * 256; idx += T) {
+        const int sm = idx >> 8;  // ss * MT + mt
+        const int ss = sm / MT;
+        const int mt = sm - ss * MT;
+        const int llo = idx & 15;
+        const int r = (idx >> 4) & 3;
+        const int lhi = (idx >> 6) & 3;
+        const int m = mt * 16 + lhi * 4 + r;
+        const int st = s0 + ss;
+        if (m >= M || st >= NS) continue;
+        const int L = lhi * 16 + llo;
+        const int n = st * kStripN + llo;
+        if constexpr (BF) {
+          uint16_t o = bf16_rne(wave_sum(sm, L, r));
+          if (bias != nullptr) o = bf16_rne(bf16_f32(o) + bf16_f32(bias[n]));
+          y[(size_t)m * ldy + n] = o;
+          continue;
+        }
+        if (MODE == kRegSingle && gridDim.y > 1) {  // this split's fp32 plane
+          part[((size_t)split * M + m) * N + n] = wave_sum(sm, L, r);
+          continue;
+        }
+        _Float16 out = (_Float16)wave_sum(sm, L, r);
+        if (bias != nullptr) out = out + as_h(bias[n]);
+        if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
+        y[(size_t)m * ldy + n] = h_bits(out);
       }
-      _Float16 out = (_Float16)wave_sum(sm, L, r);
-      if (bias != nullptr) out = out + as_h(bias[n]);
-      if (res != nullptr) out = out + as_h(res[(size_t)m * ldres + n]);
-      y[(size_t)m * ldy + n] = h_bits(out);
     }
   }
 }
@@ -779,8 +842,8 @@ static hipError_t launch_decode_reg_w(const GroupArgs& g, const RegSplit& sp, hi
 template <int MT, int MODE>
 static hipError_t launch_decode_reg_mt(const GroupArgs& g, const DecodePlan& p,
                                        const RegSplit& sp, hipStream_t stream) {
-  if (p.ss == 4) {
-    if constexpr (MODE == kRegSingle) return launch_decode_reg_w<MT, 8, 4, MODE>(g, sp, stream);
+  if (p.ss == 4) {  // planned for one to three row tiles only
+    if constexpr (MODE == kRegSingle && MT <= 3) return launch_decode_reg_w<MT, 8, 4, MODE>(g, sp, stream);
     else return hipErrorInvalidValue;
   }
   return p.ss == 2 ? launch_decode_reg_w<MT, 8, 2, MODE>(g, sp, stream)

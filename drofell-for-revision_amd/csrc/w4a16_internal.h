@@ -167,7 +167,9 @@ inline DecodePlan plan_decode(int m, int k, int n, int gs, int cus, bool single 
       double best = decode_reg_cost(m, kc, strips, r.ss, 1, gpc, cus);
       const int sss[3] = {1, 2, 4};
       for (int ss : sss) {
-        if (ss == 4 && mt >= 3 && gpc > 1) continue;  // not instantiated
+        // not instantiated: four strips of three row tiles with small groups,
+        // and of four row tiles (its registers spill)
+        if (ss == 4 && (mt == 4 || (mt >= 3 && gpc > 1))) continue;
         for (int sp = 1; sp <= 8 && sp * 8 <= kc; sp *= 2) {
           const double c = decode_reg_cost(m, kc, strips, ss, sp, gpc, cus);
           if (c < best) {

@@ -758,3 +758,15 @@ def test_output_argument_contract(hip_device):
             q4.matmul(x, output=torch.empty(m, 4095, dtype=torch.float16, device=hip_device))
         with pytest.raises(ValueError):
             q4.matmul(x, output=torch.empty(4096, m, dtype=torch.float16, device=hip_device).t())
+    for m in (1, 5):
+        say(f"output contract bf16 native M={m}, row-strided x and output")
+        xb = make_x(m, 4096, seed=m + 950).to(torch.bfloat16).to(hip_device)
+        ref = q4.matmul(xb)
+        wide = torch.zeros(m, 4096 + 24, dtype=torch.bfloat16, device=hip_device)
+        wide[:, 16:16 + 4096] = xb  # ldx = 4120 (a multiple of 8), base 32 bytes in
+        big = torch.full((m, 4096 + 64), -7.0, dtype=torch.bfloat16, device=hip_device)
+        view = big[:, 32:32 + 4096]
+        got = q4.matmul(wide[:, 16:16 + 4096], output=view)
+        torch.cuda.synchronize()
+        assert got is view and torch.equal(view.view(torch.int16), ref.view(torch.int16))
+        assert bool((big[:, :32] == -7.0).all()) and bool((big[:, 32 + 4096:] == -7.0).all())
