@@ -884,6 +884,15 @@ hipError_t launch_decode_reg(const GroupArgs& g, const DecodePlan& p, float* par
   return hipErrorInvalidValue;
 }
 
+template <int MT>
+static hipError_t launch_decode_reg_bf16_mt(const GroupArgs& g, const DecodePlan& p,
+                                            const RegSplit& sp, hipStream_t stream) {
+  if (p.ss == 1) return launch_decode_reg_w<MT, 8, 1, kRegBf16>(g, sp, stream);
+  // four row tiles of two strips are not planned (they spill)
+  if constexpr (MT <= 3) return launch_decode_reg_w<MT, 8, 2, kRegBf16>(g, sp, stream);
+  else return hipErrorInvalidValue;
+}
+
 hipError_t launch_decode_reg_bf16(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {
   if (a.M < 1 || a.M > kBf16MaxM || !p.reg || p.splits != 1 || a.res != nullptr)
     return hipErrorInvalidValue;
@@ -891,10 +900,15 @@ hipError_t launch_decode_reg_bf16(const GemmArgs& a, const DecodePlan& p, hipStr
   g.count = 1;
   g.a[0] = a;
   const RegSplit sp{1, a.K / kChunkK, nullptr};
-  if (p.waves == 16) return launch_decode_reg_w<1, 16, 1, kRegBf16>(g, sp, stream);
+  if (p.waves == 16) {
+    if (a.M > 16) return hipErrorInvalidValue;
+    return launch_decode_reg_w<1, 16, 1, kRegBf16>(g, sp, stream);
+  }
   if (p.waves != 8) return hipErrorInvalidValue;
-  return p.ss == 2 ? launch_decode_reg_w<1, 8, 2, kRegBf16>(g, sp, stream)
-                   : launch_decode_reg_w<1, 8, 1, kRegBf16>(g, sp, stream);
+  if (a.M <= 16) return launch_decode_reg_bf16_mt<1>(g, p, sp, stream);
+  if (a.M <= 32) return launch_decode_reg_bf16_mt<2>(g, p, sp, stream);
+  if (a.M <= 48) return launch_decode_reg_bf16_mt<3>(g, p, sp, stream);
+  return launch_decode_reg_bf16_mt<4>(g, p, sp, stream);
 }
 
 hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipStream_t stream) {

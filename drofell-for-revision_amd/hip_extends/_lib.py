@@ -126,8 +126,8 @@ SIGNATURES = {
     "dw4_gemm_chain": (_c.c_int, [_CPP, _P, _P]),
     "dw4_chain_timed_out": (_c.c_int, [_P, _c.POINTER(_c.c_int)]),
 }
-ABI_VERSION = 10
-BF16_MAX_M = 16  # DW4_BF16_MAX_M
+ABI_VERSION = 11
+BF16_MAX_M = 64  # DW4_BF16_MAX_M
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None

@@ -137,13 +137,6 @@ def _output_rows(output: torch.Tensor, m: int, n: int, dtype: torch.dtype) -> to
     raise ValueError("output must be contiguous or a [m, n] view with unit column stride")
 
 
-# bf16 activations up to this many rows run the packed-weight bf16 decode
-# launch (blocks of _lib.BF16_MAX_M rows, each launch reading the weights
-# once): measured faster than dequantise + a bf16 library GEMM on the 7B and
-# 13B act-order shapes through M = 64; above it the dense route.
-BF16_NATIVE_MAX_M = 64
-
-
 def _aligned_rows(x2: torch.Tensor) -> torch.Tensor:
     """A [M, K] fp16 or bf16 view whose base is 16-byte aligned with ldx % 8 == 0."""
     if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
@@ -349,16 +342,15 @@ class Q4MatrixV2(object):
           library GEMM); otherwise the HIP W4A16 kernel (decode kernel for
           small M, MFMA prefill kernel above);
         * bf16 x: with a reconstructed bf16 weight, ``must_blas`` or more
-          than ``BF16_NATIVE_MAX_M`` rows, the dense bf16 product (fp32
+          than ``BF16_MAX_M`` rows, the dense bf16 product (fp32
           accumulation) over the bf16 weight bf16(fp16(s * (q - z))), the
           reconstructed one or one dequantised into ``temp_weight`` / the
           shared buffer, as the reference's ``q4_matmul_blas_v2`` with
-          ``bfloat16`` does; up to ``BF16_NATIVE_MAX_M`` rows the HIP decode
+          ``bfloat16`` does; up to ``BF16_MAX_M`` rows the HIP decode
           kernel's bf16 mode (``dw4_gemm_bf16``: bf16 matrix cores over the
           packed words, the exact s * (q - z) applied per group in fp32, bf16
-          output), one launch per block of up to ``BF16_MAX_M`` rows, within
-          rounding of the dense product.  The activations keep bf16's range
-          either way.
+          output, one launch), within rounding of the dense product.  The
+          activations keep bf16's range either way.
 
         ``output`` (x's dtype, ``M * N`` elements, contiguous or a row-strided
         [M, N] view) receives the product; anything else raises.  ``bias``
@@ -378,21 +370,16 @@ class Q4MatrixV2(object):
             bias = bias.to(dtype).contiguous()
         dense = self._reconstructed(dtype)
         if dtype == torch.bfloat16 and dense is None and not must_blas \
-                and 0 < m <= BF16_NATIVE_MAX_M:
+                and 0 < m <= _lib.BF16_MAX_M:
             x2 = _aligned_rows(x.reshape(m, self.height))
             if out2 is None:
                 out2 = torch.empty((m, self.width), dtype=torch.bfloat16, device=self.device)
             ws = self.cache.workspace
-            lib = _lib.load()
-            for r0 in range(0, m, _lib.BF16_MAX_M):  # blocks of up to 16 rows, one launch each
-                rows = min(_lib.BF16_MAX_M, m - r0)
-                _lib.check("dw4_gemm_bf16", lib.dw4_gemm_bf16(
-                    rows, self.height, self.width, self.group_size,
-                    x2.data_ptr() + r0 * x2.stride(0) * 2, x2.stride(0),
-                    self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
-                    _ptr(self.perm) if self.use_act else None, _ptr(bias),
-                    out2.data_ptr() + r0 * out2.stride(0) * 2, out2.stride(0),
-                    ws.data_ptr(), ws.numel(), _stream(self.device)))
+            _lib.check("dw4_gemm_bf16", _lib.load().dw4_gemm_bf16(
+                m, self.height, self.width, self.group_size, x2.data_ptr(), x2.stride(0),
+                self.qweight.data_ptr(), self.qzeros.data_ptr(), self.scales.data_ptr(),
+                _ptr(self.perm) if self.use_act else None, _ptr(bias),
+                out2.data_ptr(), out2.stride(0), ws.data_ptr(), ws.numel(), _stream(self.device)))
             return out2.view(outshape) if output is None else output
         if dense is not None or must_blas or dtype == torch.bfloat16:
             w = dense if dense is not None else self._dense_weight(temp_weight, dtype)

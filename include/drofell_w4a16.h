@@ -104,7 +104,7 @@
 extern "C" {
 #endif
 
-#define DW4_ABI_VERSION 10
+#define DW4_ABI_VERSION 11
 
 enum {
   DW4_OK = 0,
@@ -176,14 +176,15 @@ int dw4_gemm(int m, int k, int n, int group_size,
  * rounding) for bf16 activations x and a bf16 output y, 1 <= m <=
  * DW4_BF16_MAX_M; larger m returns DW4_ERR_UNSUPPORTED (the caller keeps
  * the dense route: dw4_dequant_bf16, then a bf16 library GEMM).  One
- * register-fed decode launch on bf16 matrix cores, fp32 accumulation over
+ * register-fed decode launch on bf16 matrix cores (every row tile of 16 rows
+ * in the same launch, the packed weights read once), fp32 accumulation over
  * the exact integers q - z and the fp16 scales applied per group in fp32, so
  * the product is within rounding of the dense route's (whose weight is
  * rounded to bf16 first).  Same buffers, alignment and perm as dw4_gemm;
  * act-order calls use the workspace of dw4_workspace_size(m, ...) for x
  * gathered into the packed row order when it has room (otherwise every
  * workgroup gathers, same result); no K split. */
-#define DW4_BF16_MAX_M 16
+#define DW4_BF16_MAX_M 64
 int dw4_gemm_bf16(int m, int k, int n, int group_size,
                   const uint16_t* x, int64_t ldx,
                   const int32_t* packed_qweight, const int32_t* packed_zeros,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
     for name in names:
         assert hasattr(lib, name), name
-    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 10
+    assert lib.dw4_abi_version() == _lib.ABI_VERSION == 11
 
 
 def test_strerror_names_every_status():

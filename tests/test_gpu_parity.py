@@ -16,8 +16,7 @@ import torch
 
 from gptq_synth import make_layer, make_x
 from hip_extends import _lib
-from hip_extends.w4a16 import (BF16_NATIVE_MAX_M, CacheV2, Q4MatrixV2, TuningParams,
-                                gemm_group)
+from hip_extends.w4a16 import CacheV2, Q4MatrixV2, TuningParams, gemm_group
 from oracle import gptq
 
 pytestmark = pytest.mark.gpu
@@ -688,16 +687,17 @@ def test_bf16_route_beyond_fp16_range(hip_device, act):
     (5120, 5120, 128, False, True),    # act-order, x gathered into the workspace
     (1024, 768, 32, False, False),     # groups of 32 (four per chunk), waves without chunks
     (768, 512, 64, False, True),       # groups of 64, act-order, six chunks
-], ids=["4096sq", "4096x11008", "11008x4096_sym", "5120sq_act", "g32", "g64_act"])
+    (1024, 8192, 64, False, False),    # groups of 64, two strips per workgroup up to 48 rows
+], ids=["4096sq", "4096x11008", "11008x4096_sym", "5120sq_act", "g32", "g64_act", "g64_wide"])
 def test_bf16_native_decode(hip_device, k, n, g, sym, act):
-    """bf16 activations at 1 <= M <= BF16_NATIVE_MAX_M take dw4_gemm_bf16 (the
-    register-fed kernel's bf16 mode, one launch per block of up to
-    BF16_MAX_M rows): within the GEMM tolerance of the float64 product of x
-    with the dense route's weight bf16(fp16(s(q - z))) and with the exact
-    fp16 weight, bias added after the bf16 rounding, equal bits on a repeat;
-    q4.matmul returns exactly what the C entry point writes block by block;
-    act-order without workspace room (every workgroup gathering) gives the
-    same bits; one row past the native limit takes the dense route."""
+    """bf16 activations at 1 <= M <= BF16_MAX_M take dw4_gemm_bf16 (the
+    register-fed kernel's bf16 mode, one to four 16-row tiles in one launch):
+    within the GEMM tolerance of the float64 product of x with the dense
+    route's weight bf16(fp16(s(q - z))) and with the exact fp16 weight, bias
+    added after the bf16 rounding, equal bits on a repeat; q4.matmul returns
+    exactly what the C entry point writes; act-order without workspace room
+    (every workgroup gathering) gives the same bits; one row past the limit
+    takes the dense route."""
     lay, w = oracle_w(k, n, g, 7100 + k + n, sym, act)
     a = lay.numpy()
     wb = gptq.bf16_to_float(gptq.dequantize_bf16(a["qweight"], a["qzeros"], a["scales"],
@@ -706,8 +706,7 @@ def test_bf16_native_decode(hip_device, k, n, g, sym, act):
     bias = (torch.randn(n, generator=torch.Generator().manual_seed(8)) * 0.5).to(torch.bfloat16)
     bd = bias.to(hip_device)
     lib = _lib.load()
-    for m in (1, 3, 8, _lib.BF16_MAX_M, _lib.BF16_MAX_M + 1, 40, BF16_NATIVE_MAX_M,
-              BF16_NATIVE_MAX_M + 1):
+    for m in (1, 3, 8, 16, 17, 32, 40, 49, _lib.BF16_MAX_M, _lib.BF16_MAX_M + 1):
         say(f"bf16 native {k}x{n} g={g} sym={sym} act={act} M={m}")
         x = make_x(m, k, seed=m + 7).to(torch.bfloat16)
         xd = x.to(hip_device)
@@ -719,18 +718,16 @@ def test_bf16_native_decode(hip_device, k, n, g, sym, act):
         xb = x.double().numpy()
         check_tol(y.float(), xb @ wb + bias.double().numpy(), f"bf16 M={m} vs bf16 weight")
         check_tol(y.float(), xb @ w + bias.double().numpy(), f"bf16 M={m} vs fp16 weight")
-        if m > BF16_NATIVE_MAX_M:
+        if m > _lib.BF16_MAX_M:
             continue
         perm = q4.perm.data_ptr() if q4.use_act else None
         for ws, ws_bytes in ((q4.cache.workspace.data_ptr(), q4.cache.workspace.numel()),
                              (None, 0)):
             direct = torch.empty(m, n, dtype=torch.bfloat16, device=hip_device)
-            for r0 in range(0, m, _lib.BF16_MAX_M):
-                rows = min(_lib.BF16_MAX_M, m - r0)
-                _lib.check("dw4_gemm_bf16", lib.dw4_gemm_bf16(
-                    rows, k, n, g, xd[r0:].data_ptr(), k, q4.qweight.data_ptr(),
-                    q4.qzeros.data_ptr(), q4.scales.data_ptr(), perm, bd.data_ptr(),
-                    direct[r0:].data_ptr(), n, ws, ws_bytes, None))
+            _lib.check("dw4_gemm_bf16", lib.dw4_gemm_bf16(
+                m, k, n, g, xd.data_ptr(), k, q4.qweight.data_ptr(), q4.qzeros.data_ptr(),
+                q4.scales.data_ptr(), perm, bd.data_ptr(), direct.data_ptr(), n, ws, ws_bytes,
+                None))
             torch.cuda.synchronize()
             assert torch.equal(direct.view(torch.int16), y.view(torch.int16)), \
                 f"M={m} workspace={ws is not None}"
@@ -763,7 +760,7 @@ def test_output_argument_contract(hip_device):
             q4.matmul(x, output=torch.empty(m, 4095, dtype=torch.float16, device=hip_device))
         with pytest.raises(ValueError):
             q4.matmul(x, output=torch.empty(4096, m, dtype=torch.float16, device=hip_device).t())
-    for m in (1, 5):
+    for m in (1, 5, 37):
         say(f"output contract bf16 native M={m}, row-strided x and output")
         xb = make_x(m, 4096, seed=m + 950).to(torch.bfloat16).to(hip_device)
         ref = q4.matmul(xb)
