@@ -460,7 +460,7 @@ int dw4_gemm_bf16(int m, int k, int n, int group_size, const uint16_t* x, int64_
       a.perm = nullptr;
     }
   }
-  return status_of(dw4::launch_decode_reg_bf16(a, dw4::plan_decode_bf16(m, k, n, cu_count()), s));
+  return status_of(dw4::launch_decode_reg_bf16(a, dw4::plan_decode_bf16(m, k, n, group_size, cu_count()), s));
 }
 
 int dw4_dequant(int k, int n, int group_size, const int32_t* packed_qweight,

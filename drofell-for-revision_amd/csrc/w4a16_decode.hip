@@ -812,9 +812,10 @@ static hipError_t launch_decode_reg_g(const GroupArgs& g, const Items& d, const 
   const int gs = g.a[0].gs;
   const int gpc = gs >= kChunkK ? 1 : kChunkK / gs;
   if (gpc == 1) return launch_decode_reg_u<MT, WAVES, SS, 1, ACT, MODE>(g, d, sp, stream);
-  // four strips of three or four row tiles hold one group per chunk only
-  // (more per-chunk scale and zero words do not fit the registers)
-  if constexpr (SS == 4 && MT >= 3) {
+  // four strips of three or four row tiles, and the bf16 mode's two strips
+  // of four row tiles, hold one group per chunk only (more per-chunk scale
+  // and zero words do not fit the registers)
+  if constexpr ((SS == 4 && MT >= 3) || (MODE == kRegBf16 && SS == 2 && MT == 4)) {
     return hipErrorInvalidValue;
   } else {
     if (gpc == 2) return launch_decode_reg_u<MT, WAVES, SS, 2, ACT, MODE>(g, d, sp, stream);
@@ -888,9 +889,7 @@ template <int MT>
 static hipError_t launch_decode_reg_bf16_mt(const GroupArgs& g, const DecodePlan& p,
                                             const RegSplit& sp, hipStream_t stream) {
   if (p.ss == 1) return launch_decode_reg_w<MT, 8, 1, kRegBf16>(g, sp, stream);
-  // four row tiles of two strips are not planned (they spill)
-  if constexpr (MT <= 3) return launch_decode_reg_w<MT, 8, 2, kRegBf16>(g, sp, stream);
-  else return hipErrorInvalidValue;
+  return launch_decode_reg_w<MT, 8, 2, kRegBf16>(g, sp, stream);
 }
 
 hipError_t launch_decode_reg_bf16(const GemmArgs& a, const DecodePlan& p, hipStream_t stream) {

@@ -267,16 +267,17 @@ hipError_t launch_decode_pair(const GroupArgs& g, uint16_t* h, int64_t ldh, hipS
 // bf16 activations and output, 1 <= M <= kBf16MaxM, one matrix: the
 // register-fed kernel's bf16 mode, unsplit, ceil(M / 16) row tiles in one
 // launch (the weights are read once for every row).  Two strips per
-// workgroup where the strips fill the CUs twice (up to 48 rows: four row
-// tiles of two strips spill); up to 16 rows, 16 waves where one strip per
-// workgroup leaves every wave two chunks or more.
+// workgroup where the strips fill the CUs twice (four row tiles only with
+// one group per chunk: with more groups' scale and zero words they spill);
+// up to 16 rows, 16 waves where one strip per workgroup leaves every wave
+// two chunks or more.
 constexpr int kBf16MaxM = 64;  // DW4_BF16_MAX_M of the public header
-inline DecodePlan plan_decode_bf16(int m, int k, int n, int cus) {
+inline DecodePlan plan_decode_bf16(int m, int k, int n, int gs, int cus) {
   const int kc = k / kChunkK;
   const int strips = n / kStripN;
   DecodePlan r{1, kc, 8, 0};
   r.reg = true;
-  r.ss = (m <= 48 && strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
+  r.ss = ((m <= 48 || gs >= kChunkK) && strips % 2 == 0 && strips / 2 >= cus) ? 2 : 1;
   if (m <= 16 && r.ss == 1 && strips <= cus && kc >= 32) r.waves = 16;
   r.smem = (size_t)r.waves * r.ss * 64 * 16;
   return r;
