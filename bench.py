@@ -127,7 +127,9 @@ def time_graph(mats, m: int, steps: int, warmup: int, dev, select=None, per_repl
     return ms, wall, sel
 
 
-DECODE_SOURCES = ("w4a16_decode.hip", "w4a16_internal.h", "w4a16_device.h")
+# The decode kernel's sources and the Makefile (whose flags for
+# w4a16_decode.hip change the generated code).
+DECODE_SOURCES = ("w4a16_decode.hip", "w4a16_internal.h", "w4a16_device.h", "Makefile")
 
 
 def decode_source_sha256() -> str:

@@ -151,6 +151,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_NAME} is not built ({path} missing); run "
                 "`make -C drofell-for-revision_amd/csrc` or __graft_entry__.build()")
+        # torch first: its wheel carries its own HIP runtime, and the library's
+        # libamdhip64.so.7 dependency binds to the one already loaded.  Loaded
+        # before torch, the library would bring in the system runtime and the
+        # process would hold two (kernel launches then fail, and pointers and
+        # streams from torch would belong to the other runtime).
+        import torch  # noqa: F401
         lib = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
