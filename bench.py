@@ -810,6 +810,71 @@ def sweep(mats, dev, steps: int, warmup: int,
     return out
 
 
+def bf16_sweep(dev, steps: int, warmup: int,
+               plan=(((4096, 4096), False), ((4096, 11008), False), ((11008, 4096), False),
+                     ((5120, 5120), True)),
+               ms_list=(1, 8, 16, 17, 32, 48, 64)) -> list:
+    """bf16 activations through Q4MatrixV2.matmul: the packed-weight bf16
+    decode launch (dw4_gemm_bf16) against the dense route (bf16
+    dequantisation, then a bf16 library GEMM; must_blas), microseconds per
+    call.  Each shape rotates over distinct matrices totalling at least
+    256 MB (so no call finds its weights in the Infinity Cache), every call
+    writing a preallocated output, captured in one HIP graph per (shape, M,
+    route) and replayed steps times after warmup replays.  JSON lines on
+    stderr; returns them."""
+    import torch
+    from gptq_synth import algorithmic_bytes
+
+    out = []
+    for (k, n), act in plan:
+        count = max(4, -(-(256 << 20) // (k * n // 2)))
+        mats, cache = build_matrices(dev, count, 64, seed0=500, shapes={"p": (k, n)},
+                                     act_order=act)
+        for m in ms_list:
+            gen = torch.Generator(device=dev)
+            gen.manual_seed(m)
+            x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            us = {}
+            for route, dense in (("native", False), ("dense", True)):
+                def one():
+                    for _, _, _, q4 in mats:
+                        q4.matmul(x, output=y, must_blas=dense)
+
+                side = torch.cuda.Stream(device=dev)
+                side.wait_stream(torch.cuda.current_stream(dev))
+                with torch.cuda.stream(side):
+                    one()  # first calls (library handles, dequantisation buffers) outside capture
+                torch.cuda.current_stream(dev).wait_stream(side)
+                torch.cuda.synchronize(dev)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    one()
+                for _ in range(warmup):
+                    g.replay()
+                torch.cuda.synchronize(dev)
+                s = torch.cuda.current_stream(dev)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(s)
+                for _ in range(steps):
+                    g.replay()
+                b.record(s)
+                torch.cuda.synchronize(dev)
+                us[route] = a.elapsed_time(b) / steps * 1e3 / len(mats)
+                del g
+            nbytes = algorithmic_bytes(m, k, n, GROUP, act)
+            rec = {"shape": f"{k}x{n}", "act_order": act, "m": m, "matrices": len(mats),
+                   "native_us": round(us["native"], 2), "dense_us": round(us["dense"], 2),
+                   "speedup": round(us["dense"] / us["native"], 2),
+                   "native_GB/s": round(nbytes / us["native"] / 1e3, 1)}
+            log(json.dumps(rec))
+            out.append(rec)
+        del mats, cache
+        torch.cuda.empty_cache()
+    return out
+
+
 # The benchmark's configurations 1-4 as the default run measures them: (tag,
 # shape, act-order, symmetric zeros, M values).  Configuration 5 is the stage
 # leg.
@@ -890,6 +955,9 @@ def main() -> int:
                          "shapes and exit")
     ap.add_argument("--crossover", action="store_true",
                     help="only time the 56-matrix pass native vs dense routes over M and exit")
+    ap.add_argument("--bf16-sweep", action="store_true",
+                    help="only time bf16 activations through the packed-weight bf16 decode "
+                         "launch against the dense route over shapes and M, and exit")
     ap.add_argument("--peaks", action="store_true",
                     help="only time a large fp16 library GEMM, a 1 GiB copy and a 1 GiB "
                          "streaming read on this box, print them and exit")
@@ -921,6 +989,9 @@ def main() -> int:
         return 0
     if args.peaks:
         device_peaks(dev, args.steps)
+        return 0
+    if args.bf16_sweep:
+        bf16_sweep(dev, args.steps, args.warmup)
         return 0
     log(f"building {args.layers} layers x {len(LLAMA2_7B_SHAPES)} projections")
     mats, _cache = build_matrices(dev, args.layers, max(args.prefill_m, 1))
