@@ -56,11 +56,14 @@ __device__ __forceinline__ h8 centered8(uint32_t w, h2 nz1024, h2 nz64, uint32_t
 
 // Zero-point constants -(1024 + z_eff) and -(64 + z_eff) (z_eff = stored + 1,
 // 1..16) built from their fp16 bit patterns: 1024 + z has exponent 10 and
-// mantissa z, 64 + z has exponent 6 and mantissa 16 z.
+// mantissa z, 64 + z has exponent 6 and mantissa 16 z.  With the stored
+// nibble zs the patterns are 0xE401 + zs and 0xD410 + 16 zs (no carry out of
+// a half-word: at most 0xE410 and 0xD500), so each is one multiply-add over
+// both halves.
 __device__ __forceinline__ void zero_consts(uint32_t zword, int zshift, h2& nz1024, h2& nz64) {
-  const uint32_t ze = ((zword >> zshift) & 15u) + 1u;
-  nz1024 = as_h2((0xE400u | ze) * 0x00010001u);
-  nz64 = as_h2((0xD400u | (ze << 4)) * 0x00010001u);
+  const uint32_t zs = (zword >> zshift) & 15u;
+  nz1024 = as_h2(zs * 0x00010001u + 0xE401E401u);
+  nz64 = as_h2(zs * 0x00100010u + 0xD410D410u);
 }
 
 // Wait until every vector memory operation this wave has issued has
