@@ -328,7 +328,7 @@ chain_kernel(const ChainLinkDev* __restrict__ links, ChainHeader* hdr, uint64_t*
   const int kq = lane >> 4;
   const int hsh = (j & 1) * 16;
   const int zsh = (j & 7) * 4;
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   unsigned char* ring = rings + (size_t)ws * R * kSlot;
   const uint32_t ring0 = lds_addr(ring);
 

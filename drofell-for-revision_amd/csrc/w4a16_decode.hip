@@ -231,7 +231,7 @@ decode_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Items d,
   // complete in order, so no workgroup barrier is needed here.
 
   const int zsh = (j & 7) * 4;
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   // A-operand rows: lanes past the last row read row M-1.  Output row i of
   // an MFMA depends only on A row i, and rows >= M are never stored.
   int xrow[MT];
@@ -483,7 +483,7 @@ decode_reg_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const Item
   for (int ss = 0; ss < SS; ++ss)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) tot[ss][mt] = f4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t magic = BF ? kMagicBf16 : kMagic;
+  const uint32_t magic = opaque(BF ? kMagicBf16 : kMagic);
   const u4 ones_bf16 = u4{kOnesBf16, kOnesBf16, kOnesBf16, kOnesBf16};
   auto consume = [&](int slot_u) {
     if constexpr (LX) {  // the slot's registers go out in load order, come back in operand order

@@ -23,18 +23,25 @@ __device__ __forceinline__ _Float16 as_h(uint16_t u) { return __builtin_bit_cast
 __device__ __forceinline__ uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 __device__ __forceinline__ h2 splat2(_Float16 v) { return h2{v, v}; }
 
-// (a & mask) | magic in one v_and_or_b32 (mask in an SGPR, magic in a
-// VGPR).  magic first passes through an empty assembly statement that hides
-// its constant value: with both constants known the compiler would emit two
-// instructions (a gfx9 VOP3 instruction cannot encode literals).  The
-// v_and_or_b32 itself stays the compiler's, so its hazard recognizer sees the
-// register write and keeps the wait states the matrix cores need around it
-// (an MFMA reading a VALU result; a VALU overwriting the SrcC or the
-// destination of an MFMA in flight).  Written as assembly, the instruction
-// was invisible to it: results then fed MFMAs, or overwrote an in-flight
-// MFMA's SrcC, closer than those wait states.
+// A constant the compiler can no longer see: the value passes through an
+// empty assembly statement that leaves it in a VGPR.  Kernels make their
+// dequantisation magic opaque once, at the start, so that and_or below is one
+// v_and_or_b32 (mask in an SGPR, magic in that VGPR): with both constants
+// known the compiler would emit two instructions (a gfx9 VOP3 instruction
+// cannot encode literals), and hiding it per call re-creates the constant in
+// a VGPR once per chunk.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+// (a & mask) | magic, magic from opaque().  The v_and_or_b32 is the
+// compiler's, so its hazard recognizer sees the register write and keeps the
+// wait states the matrix cores need around it (an MFMA reading a VALU result;
+// a VALU overwriting the SrcC or the destination of an MFMA in flight).
+// Written as assembly, the instruction was invisible to it: results then fed
+// MFMAs, or overwrote an in-flight MFMA's SrcC, closer than those wait states.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  asm("" : "+v"(magic));
   return (a & mask) | magic;
 }
 

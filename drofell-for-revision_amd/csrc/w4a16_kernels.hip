@@ -214,7 +214,7 @@ prefill_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
     for (int si = 0; si < S; ++si) acc[mt][si] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   // One workgroup per CU, one wave per SIMD: a wave has to hide its own
   // latencies, so the four 32-row k-steps of a chunk are software pipelined
   // -- while the MFMAs of step t run, the wave reads the A fragments of step
@@ -554,7 +554,7 @@ prefill32_kernel(const _Float16* __restrict__ x, int64_t ldx, int M,
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mt][p][e] = 0.f;
 
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   // Software pipeline over the 8 k-steps of a chunk: the region of step t
   // holds the MFMAs of step t (operands dequantised in the previous region)
   // and the dequantisation and A-fragment reads of step t+1, independent

@@ -277,7 +277,7 @@ prefill2_kernel(const _Float16* __restrict__ x, int64_t ldx, int M, const P2Item
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[mt][p][e] = 0.f;
 
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   const int hsh = (j & 1) * 16;
   const int zsh = (j & 7) * 4;
   const int gbase = (step0 * GPC) / 8;  // first group of the chunk this wave's slice uses

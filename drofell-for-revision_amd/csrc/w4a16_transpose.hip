@@ -109,7 +109,7 @@ gemm_t_kernel(const _Float16* __restrict__ g, int64_t ldg, int M,
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[kb][mt] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t magic = kMagic;
+  const uint32_t magic = opaque(kMagic);
   const int hsh = (j & 1) * 16;
   const int zsh = (j & 7) * 4;
   constexpr int WPG = 4 / GPC;  // packed words (32-row k-steps) per group
